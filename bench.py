@@ -1,0 +1,400 @@
+#!/usr/bin/env python3
+"""Benchmark of the per-layer expert-cache path on one MI355X.
+
+Workload: 48 MoE layers x 128 W8A8 experts (4,732,928 B each: int8 w13 [1536, 2048], int8
+w2 [2048, 768], fp32 scales [1536, 1] and [2048, 1]), ~29 GB of pinned host memory, top-8
+routing at decode batch 1 (Zipf 1.1 with 0.6 per-expert repeat, one seed per layer), 64 HBM
+slots per layer, LFU with decay 64, 4096-step trace. One "step" is one decode step across
+all 48 layers: per layer, the fused policy step + remap kernel and the gather kernel, as the
+plugin launches them, captured once into a HIP graph and replayed per step (the way vLLM
+runs decode). Routing ids for the step are copied into the graph's input buffer first.
+
+Printed (one JSON line on stdout):
+  value        gathered bytes / wall time of the timed steps (GB/s), sources in host memory
+  roofline     the gather kernel: achieved host->HBM GB/s (algorithmic bytes / kernel time,
+               HIP events on the launch stream over a window of the timed steps) against
+               the measured host->device link peak
+  manage_remap_us_per_layer   mean duration of the fused policy+remap kernel
+  hit_rate     1 - inserts / distinct routed experts over the timed steps
+  cpu_baseline the CPU path on this box's host: the policy restated in C (oracle/) on one
+               core deciding the misses, and one hipMemcpyAsync per (miss, buffer), on a
+               sample of the same steps
+
+    python bench.py [--steps K] [--warmup W] [--slots 64] [--policy lfu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "vllm-expert-cache_amd"))
+
+METRIC = ("host->HBM gather GB/s (% link peak); manage+remap µs/layer; hit rate")
+WORKLOAD = "48-layer-e128"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=4032)
+    p.add_argument("--warmup", type=int, default=64)
+    p.add_argument("--slots", type=int, default=64)
+    p.add_argument("--policy", choices=("lfu", "lru"), default="lfu")
+    p.add_argument("--layers", type=int, default=48)
+    p.add_argument("--timing-window", type=int, default=32,
+                   help="timed steps re-run with per-kernel HIP events")
+    p.add_argument("--cpu-steps", type=int, default=512,
+                   help="timed steps in the CPU-baseline sample (0 to skip)")
+    p.add_argument("--chunks", type=int, default=None)
+    p.add_argument("--lanes", type=int, default=None)
+    return p.parse_args()
+
+
+class Layers:
+    """Device state of every layer's cache, one row per layer."""
+
+    def __init__(self, torch, L, E, S, dev):
+        i32, i64 = torch.int32, torch.int64
+        self.table = torch.full((L, E), -1, dtype=i32, device=dev)
+        self.map_cold = torch.arange(E, dtype=i32, device=dev).repeat(L, 1)
+        self.slot_expert = torch.full((L, S), -1, dtype=i32, device=dev)
+        self.slot_stamp = torch.zeros((L, S), dtype=i64, device=dev)
+        self.routed = torch.zeros((L, E), dtype=torch.uint8, device=dev)
+        self.step = torch.zeros((L, 1), dtype=i64, device=dev)
+        self.miss = torch.zeros((L, 2 * S), dtype=i32, device=dev)
+        self.fields = ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "step",
+                       "miss")
+
+    def row(self, name, l):
+        t = getattr(self, name)
+        return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
+
+    def snapshot(self):
+        return {f: getattr(self, f).clone() for f in self.fields}
+
+    def restore(self, snap):
+        for f in self.fields:
+            getattr(self, f).copy_(snap[f])
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this path has no cross-GPU work (each tensor-"
+              f"parallel rank runs its own identical cache); --gpus {args.gpus} is not "
+              f"supported", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from vllm_expert_cache import _lib, traces
+    from vllm_expert_cache.cache import DEFAULT_CHUNKS, DEFAULT_LANES
+
+    lib = _lib.lib()  # raises if the HIP library is missing: there is no fallback
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = traces.WORKLOADS[WORKLOAD]
+    L, E, S, mk = args.layers, w.experts, args.slots, w.mk
+    policy = 1 if args.policy == "lfu" else 0
+    decay = 64
+    chunks = args.chunks or DEFAULT_CHUNKS
+    lanes = args.lanes or DEFAULT_LANES
+    W, K = args.warmup, args.steps
+    T = W + K
+    bufs = [b.nbytes for b in w.buffers]
+    B_exp = sum(bufs)
+
+    # ---- routing and host expert store --------------------------------------------------
+    t0 = time.time()
+    ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)  # [T, L, mk]
+    ids_dev = torch.as_tensor(ids_np, device=dev)
+    host = []  # host[l][b]: pinned [E * bytes_b]
+    for l in range(L):
+        host.append([torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs])
+    slots = [[torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
+             for _ in range(L)]
+    log(f"setup: routing {ids_np.shape}, host store {L * E * B_exp / 1e9:.1f} GB pinned, "
+        f"slots {L * S * B_exp / 1e9:.1f} GB, {time.time() - t0:.1f}s")
+
+    st = Layers(torch, L, E, S, dev)
+    ids_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+    out_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+    nm_static = torch.zeros((L,), dtype=torch.int32, device=dev)
+    nm_hist = torch.zeros((T, L), dtype=torch.int32, device=dev)
+
+    def row(t, l):
+        return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
+
+    def gather_args(l):
+        a = []
+        for i in range(6):  # pad to six buffers with a repeat, as cache.refresh does
+            j = min(i, len(bufs) - 1)
+            a += [ctypes.c_void_p(slots[l][j].data_ptr()),
+                  ctypes.c_void_p(host[l][j].data_ptr()), ctypes.c_long(bufs[j])]
+        return a
+
+    def manage_args(l, ids_p, nm_p, out_p):
+        return (ids_p, 4, mk, E, S, min(E, mk), S, st.row("table", l), st.row("map_cold", l),
+                st.row("slot_expert", l), st.row("slot_stamp", l), st.row("routed", l),
+                st.row("step", l), st.row("miss", l), nm_p, policy, decay, out_p)
+
+    M_ARGS = [manage_args(l, row(ids_static, l), row(nm_static, l), row(out_static, l))
+              for l in range(L)]
+    G_ARGS = [tuple(gather_args(l)) + (st.row("miss", l), row(nm_static, l), chunks, lanes)
+              for l in range(L)]
+
+    def launch_step(stream):
+        s = ctypes.c_void_p(stream.cuda_stream)
+        for l in range(L):
+            rc = lib.expert_cache_manage_remap(*M_ARGS[l], s)
+            rc |= lib.expert_cache_gather(*G_ARGS[l], s)
+            if rc:
+                raise RuntimeError(f"launch failed rc={rc}")
+
+    # ---- capture one decode step into a graph --------------------------------------------
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    snap0 = st.snapshot()
+    with torch.cuda.stream(side):
+        launch_step(side)  # warm-up launch outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    st.restore(snap0)
+    nm_static.zero_()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+
+    def run_steps(t_from, t_to):
+        for t in range(t_from, t_to):
+            ids_static.copy_(ids_dev[t], non_blocking=True)
+            graph.replay()
+            nm_hist[t].copy_(nm_static, non_blocking=True)
+
+    # ---- warm-up, then the timed steps -----------------------------------------------------
+    run_steps(0, W)
+    torch.cuda.synchronize()
+    snap = st.snapshot()
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev_a.record()
+    run_steps(W, T)
+    ev_b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    gpu_ms = ev_a.elapsed_time(ev_b)
+    elapsed_s = max(wall, gpu_ms / 1e3)
+    nm = nm_hist.cpu().numpy()
+    inserts = int(nm[W:T].sum())
+    distinct = sum(len(np.unique(ids_np[t, l])) for t in range(W, T) for l in range(L))
+    gathered = inserts * B_exp
+    value = gathered / elapsed_s / 1e9
+    log(f"timed: {K} steps in {elapsed_s:.2f}s ({1e3 * elapsed_s / K:.3f} ms/step), "
+        f"{inserts} inserts, {gathered / 1e9:.1f} GB -> {value:.2f} GB/s")
+
+    # ---- per-kernel durations: a window of the timed steps, HIP events per launch ---------
+    final = st.snapshot()
+    st.restore(snap)
+    win = max(1, min(args.timing_window, K))
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(win)]
+    stream = torch.cuda.current_stream()
+    s_ptr = ctypes.c_void_p(stream.cuda_stream)
+    win_out = torch.zeros((win, L, mk), dtype=torch.int32, device=dev)
+    win_nm = torch.zeros((win, L), dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(5e8))  # hold the stream while the window is queued behind it
+    for i in range(win):
+        t = W + i
+        for l in range(L):
+            e0, e1, e2 = ev[i][l]
+            e0.record(stream)
+            rc = lib.expert_cache_manage_remap(
+                *manage_args(l, row(ids_dev[t], l), row(win_nm[i], l), row(win_out[i], l)),
+                s_ptr)
+            e1.record(stream)
+            rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
+                                          row(win_nm[i], l), chunks, lanes, s_ptr)
+            e2.record(stream)
+            if rc:
+                raise RuntimeError(f"launch failed rc={rc}")
+    torch.cuda.synchronize()
+    man_us = np.array([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
+                       for i in range(win)])
+    gat_us = np.array([[ev[i][l][1].elapsed_time(ev[i][l][2]) * 1e3 for l in range(L)]
+                       for i in range(win)])
+    wnm = win_nm.cpu().numpy()
+    assert np.array_equal(wnm, nm[W:W + win]), "window replay diverged from the timed steps"
+    st.restore(final)
+    miss_launch = wnm > 0
+    win_bytes = wnm.sum() * B_exp
+    achieved = win_bytes / (gat_us.sum() * 1e-6) / 1e9
+    per_miss = (wnm[miss_launch].sum() * B_exp / (gat_us[miss_launch].sum() * 1e-6) / 1e9
+                if miss_launch.any() else None)
+    log(f"window {win} steps: manage+remap {man_us.mean():.2f} us/layer "
+        f"(p50 {np.median(man_us):.2f}), gather {gat_us.mean():.1f} us/launch, "
+        f"{achieved:.2f} GB/s over all launches, {per_miss} GB/s over launches with a miss, "
+        f"{gat_us[~miss_launch].mean() if (~miss_launch).any() else float('nan'):.2f} us "
+        f"for a launch with no miss")
+
+    # ---- host->device link peak -------------------------------------------------------------
+    n_peak = 256 << 20
+    src = torch.empty(n_peak, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(n_peak, dtype=torch.uint8, device=dev)
+    for _ in range(2):
+        dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(5):
+        dst.copy_(src, non_blocking=True)
+    b.record()
+    torch.cuda.synchronize()
+    memcpy_gbps = 5 * n_peak / (a.elapsed_time(b) * 1e-3) / 1e9
+    one = torch.tensor([0, 0], dtype=torch.int32, device=dev)
+    one_n = torch.tensor([1], dtype=torch.int32, device=dev)
+    big = [ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+           ctypes.c_long(n_peak)] * 6
+    tail = (ctypes.c_void_p(one.data_ptr()), ctypes.c_void_p(one_n.data_ptr()), chunks, lanes,
+            s_ptr)
+    for _ in range(2):
+        assert lib.expert_cache_gather(*big, *tail) == 0
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(5):
+        lib.expert_cache_gather(*big, *tail)
+    b.record()
+    torch.cuda.synchronize()
+    kernel_gbps = 5 * n_peak / (a.elapsed_time(b) * 1e-3) / 1e9
+    peak = max(memcpy_gbps, kernel_gbps)
+    log(f"link peak: hipMemcpyAsync H2D {memcpy_gbps:.2f} GB/s, gather kernel on one 256 MB "
+        f"slab {kernel_gbps:.2f} GB/s")
+
+    # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer) --------------
+    cpu = None
+    if args.cpu_steps > 0:
+        cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk,
+                           policy, decay, W, dev)
+
+    res = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(1e3 * elapsed_s / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": WORKLOAD, "layers": L, "experts": E, "top_k": w.top_k,
+                   "tokens_per_step": w.tokens, "slots": S, "policy": args.policy,
+                   "decay": decay, "bytes_per_expert": B_exp, "host_store_GB":
+                   round(L * E * B_exp / 1e9, 2), "gather_grid": [chunks, lanes],
+                   "timed_trace_steps": [W, T]},
+        "hit_rate": round(1.0 - inserts / distinct, 5),
+        "inserts": inserts,
+        "manage_remap_us_per_layer": round(float(man_us.mean()), 3),
+        "gather_us_per_launch": round(float(gat_us.mean()), 3),
+        "gather_GBps_launches_with_miss": None if per_miss is None else round(per_miss, 3),
+        "link_peak_GBps": {"hipMemcpyAsync_h2d": round(memcpy_gbps, 3),
+                           "gather_kernel_256MB": round(kernel_gbps, 3)},
+        "roofline": {"bound": "host-link", "kernel": "gather_k", "achieved": round(achieved, 3),
+                     "peak": round(peak, 3), "unit": "GB/s", "frac": round(achieved / peak, 4),
+                     "traffic": None,
+                     "achieved_def": f"gathered bytes / summed gather kernel time, {win} "
+                                     f"timed steps x {L} layers, HIP events",
+                     "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
+                                 "kernel on one 256 MB slab)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, policy, decay,
+                 W, dev):
+    """The CPU path on this host: the oracle's C policy (one core) decides each layer's
+    misses from the same start state, and each (miss, buffer) is one hipMemcpyAsync from
+    pinned host memory into the slot. Bounded sample: the first cpu_steps timed steps."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    n = min(args.cpu_steps, ids_np.shape[0] - W)
+    states = []
+    for l in range(L):
+        s = oracle.State(E, S)
+        s.table[:] = snap["table"][l].cpu().numpy()
+        s.map_cold[:] = snap["map_cold"][l].cpu().numpy()
+        s.slot_expert[:] = snap["slot_expert"][l].cpu().numpy()
+        s.slot_stamp[:] = snap["slot_stamp"][l].cpu().numpy()
+        s.step[:] = snap["step"][l].cpu().numpy()
+        states.append(s)
+    B_exp = sum(bufs)
+    # policy alone, in C, over the sample (copies of the states, so the run below is fresh)
+    pol_states = [s.copy() for s in states]
+    t0 = oracle.now()
+    for l in range(L):
+        oracle.run_trace(np.ascontiguousarray(ids_np[W:W + n, l]), E, S, policy, decay,
+                         state=pol_states[l])
+    policy_us = (oracle.now() - t0) / (n * L) * 1e6
+    torch.cuda.synchronize()
+    moved = 0
+    t0 = time.perf_counter()
+    for t in range(W, W + n):
+        for l in range(L):
+            s = states[l]
+            s.manage(ids_np[t, l], min(E, mk), S, policy, decay)
+            for j in range(int(s.n_miss[0])):
+                e, sl = int(s.miss[2 * j]), int(s.miss[2 * j + 1])
+                for i, b in enumerate(bufs):
+                    slots[l][i][sl * b:(sl + 1) * b].copy_(host[l][i][e * b:(e + 1) * b],
+                                                           non_blocking=True)
+                moved += B_exp
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    hbuf = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    hsrc = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    hbuf.copy_(hsrc)
+    t1 = time.perf_counter()
+    for _ in range(4):
+        hbuf.copy_(hsrc)
+    host_memcpy = 4 * (256 << 20) / (time.perf_counter() - t1) / 1e9
+    log(f"cpu baseline: {n} steps x {L} layers, {moved / 1e9:.2f} GB in {wall:.2f}s -> "
+        f"{moved / wall / 1e9:.2f} GB/s; policy {policy_us:.3f} us/layer-step; host memcpy "
+        f"{host_memcpy:.1f} GB/s")
+    return {"value": round(moved / wall / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"timed steps {W}..{W + n} of the trace x {L} layers from the same start "
+                      f"state: C policy (oracle/policy.c) per layer-step, then one "
+                      f"hipMemcpyAsync H2D per (miss, buffer)",
+            "policy_us_per_layer_step": round(policy_us, 4),
+            "host_memcpy_GBps": round(host_memcpy, 2),
+            "cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+if __name__ == "__main__":
+    main()

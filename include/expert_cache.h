@@ -1,0 +1,114 @@
+/*
+ * libexpertcache.so -- C-ABI of the per-MoE-layer expert cache, built for gfx950 (MI355X).
+ *
+ * Every pointer is caller-owned (device memory, or for gather sources host memory the
+ * device can read); the library allocates nothing and keeps no state. Every call is
+ * asynchronous on `stream`, reads no device value back to the host and allocates nothing,
+ * so any sequence of calls can be captured into a HIP graph.
+ *
+ * Return value: 0 on success; -1 when an argument check fails (checked on the host before
+ * any HIP call, so these paths need no GPU); otherwise the hipError_t of the launch.
+ *
+ * State of one layer's cache (what the caller allocates, vllm_expert_cache/cache.py:84-92):
+ *   table       int32[E]    expert -> slot, or -1
+ *   map_cold    int32[E]    expert -> itself when not resident, else -1
+ *   slot_expert int32[S]    slot -> expert, or -1
+ *   slot_stamp  int64[S]    slot priority: last step routed (LRU) or hit count (LFU)
+ *   routed      uint8[E]    left holding this step's routed flags
+ *   step        int64[1]    calls so far
+ *   miss        int32[2*max_inserts]  (expert, slot) pairs of this step's inserts
+ *   n_miss      int32[1]    number of pairs
+ */
+#ifndef EXPERT_CACHE_H
+#define EXPERT_CACHE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/*
+ * One policy step: mark the experts routed this step, refresh the priority of the resident
+ * ones, pick victims among the slots not needed this step (lowest (stamp, slot) first),
+ * install the missing experts in ascending id order and write the miss list.
+ * policy 0 = LRU, 1 = LFU (counts halve every `decay` steps on steps that insert).
+ * Fails with -1 unless E > 0, 0 < S <= 1024, 0 <= max_inserts <= 1024, policy in {0, 1}.
+ *
+ * Replaces: kernels/expert_cache.hip:592-603 (same signature, same checks, same results);
+ * bound by vllm_expert_cache/_lib.py:44-47.
+ */
+int expert_cache_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                        int max_inserts, int* table, int* map_cold, int* slot_expert,
+                        long long* slot_stamp, unsigned char* routed, long long* step,
+                        int* miss, int* n_miss, int policy, int decay, hipStream_t stream);
+
+/*
+ * Copy every missing expert's slabs from host-readable memory into its slot: for
+ * j < *n_miss and each of the six buffers, dst_b[slot_j] <- src_b[expert_j], b_b bytes per
+ * expert. A buffer repeated with the same (dst, src, bytes) is copied once.
+ * The grid is chunks x lanes workgroups of 256 lanes; the work (miss, buffer, tile) is
+ * spread over the whole grid whatever n_miss is.
+ * Fails with -1 unless every b_b > 0 and b_b % 16 == 0, chunks > 0 and lanes > 0.
+ *
+ * Replaces: kernels/expert_cache.hip:626-643 (same signature and checks);
+ * bound by vllm_expert_cache/_lib.py:49-53.
+ */
+int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, long b1,
+                        void* d2, const void* s2, long b2, void* d3, const void* s3, long b3,
+                        void* d4, const void* s4, long b4, void* d5, const void* s5, long b5,
+                        const int* miss, const int* n_miss, int chunks, int lanes,
+                        hipStream_t stream);
+
+/*
+ * The LRU policy step (hits and installs stamp the current step, no decay) followed by both
+ * moe_align_block_size outputs built from the updated table: the resident side bucketed by
+ * slot, the non-resident side bucketed by expert id; sentinel mk in sorted_*, -1 in unused
+ * eids_* blocks, ids outside [0, E) skipped. Within a bucket, ids are in token order.
+ * L and NB must be the lengths vLLM's wrapper allocates:
+ *   L = mk < E ? min(mk*bs, mk + E*(bs-1)) : mk + E*(bs-1),  NB = ceil(L / bs).
+ * Fails with -1 unless 0 < E <= 1024, 0 < S <= 1024, bs, L, NB > 0, mk >= 0,
+ * 0 <= max_inserts <= 1024.
+ *
+ * Replaces: kernels/expert_cache.hip:605-624 (same signature and checks).
+ */
+int expert_cache_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                       int max_inserts, int* table, int* map_cold, int* slot_expert,
+                       long long* slot_stamp, unsigned char* routed, long long* step,
+                       int* miss, int* n_miss, int bs, int L, int NB, int* sorted_hot,
+                       int* eids_hot, int* npad_hot, int* sorted_cold, int* eids_cold,
+                       int* npad_cold, hipStream_t stream);
+
+/*
+ * Routing ids from expert space to slot space: out[i] = table[ids[i]], a negative id
+ * wrapping to table[E + id] as torch indexing does. `id_bytes` is 4 (int32 ids and out) or
+ * 8 (int64 ids and out). An id outside [-E, E) (an index error in torch) gives -1.
+ * Fails with -1 unless E > 0, n >= 0 and id_bytes is 4 or 8.
+ *
+ * Replaces: vllm_expert_cache/cache.py:108-110 (`table[ids.long()].to(ids.dtype)`, three
+ * torch kernels); no counterpart in the reference's C-ABI.
+ */
+int expert_cache_remap(const void* ids, int n, int id_bytes, const int* table, int E,
+                       void* out, hipStream_t stream);
+
+/*
+ * expert_cache_manage followed by expert_cache_remap of the same ids against the updated
+ * table, in one launch. `ids` are int32 (id_bytes 4) or int64 (id_bytes 8); the policy sees
+ * each id truncated to int32, as the reference's `topk_ids.to(torch.int32)` does, and `out`
+ * receives the slot ids in the dtype of `ids`. Argument checks are those of
+ * expert_cache_manage plus id_bytes in {4, 8}.
+ *
+ * Replaces: vllm_expert_cache/cache.py:116-133 plus :163 (cast, manage, and the torch
+ * remap); no counterpart in the reference's C-ABI.
+ */
+int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int S,
+                              int max_distinct, int max_inserts, int* table, int* map_cold,
+                              int* slot_expert, long long* slot_stamp, unsigned char* routed,
+                              long long* step, int* miss, int* n_miss, int policy, int decay,
+                              void* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXPERT_CACHE_H */

@@ -1,0 +1,139 @@
+"""C-ABI of libexpertcache.so, checked without a GPU.
+
+The library loads here (libamdhip64 loads without a device), exports every entry point
+include/expert_cache.h declares, and rejects bad arguments with -1 before any HIP call --
+with the same verdicts as the reference library compiled from its own source
+(kernels/expert_cache.hip:592-643) where that is built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+
+import pytest
+
+import oracle
+from vllm_expert_cache import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "expert_cache.h"
+P = ctypes.c_void_p
+
+
+def _declared():
+    return sorted(set(re.findall(r"^int\s+(expert_cache_\w+)\s*\(", HEADER.read_text(), re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.lib()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not os.path.isfile(oracle.REF_LIB_PATH):
+        pytest.skip("reference library not built (oracle/_ref)")
+    return ctypes.CDLL(oracle.REF_LIB_PATH)
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared()
+    assert set(declared) == set(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_library_path_order(tmp_path, monkeypatch):
+    fake = tmp_path / "libexpertcache.so"
+    fake.write_bytes(b"")
+    monkeypatch.setenv("EXPERT_CACHE_LIB", str(fake))
+    assert _lib.library_path() == str(fake)
+    monkeypatch.setenv("EXPERT_CACHE_LIB", str(tmp_path / "missing.so"))
+    assert _lib.library_path().endswith("vllm_expert_cache/libexpertcache.so")
+
+
+def test_bind_refuses_a_library_without_the_remap(ref):
+    with pytest.raises(RuntimeError, match="expert_cache_remap"):
+        _lib.bind(ref)
+
+
+def _manage(h, E, S, mi, pol, name="expert_cache_manage"):
+    fn = getattr(h, name)
+    fn.restype = ctypes.c_int
+    fn.argtypes = _lib.SIGNATURES["expert_cache_manage"]
+    return fn(P(1), 1, E, S, 1, mi, P(1), P(1), P(1), P(1), P(1), P(1), P(1), P(1), pol, 64,
+              None)
+
+
+BAD_MANAGE = [(0, 4, 4, 0), (-3, 4, 4, 0), (8, 0, 4, 0), (8, 1025, 4, 0), (8, 4, -1, 0),
+              (8, 4, 1025, 0), (8, 4, 4, 2), (8, 4, 4, -1)]
+
+
+@pytest.mark.parametrize("args", BAD_MANAGE)
+def test_manage_rejects(lib, args):
+    assert _manage(lib, *args) == -1
+
+
+@pytest.mark.parametrize("args", BAD_MANAGE)
+def test_manage_rejects_like_reference(lib, ref, args):
+    assert _manage(lib, *args) == _manage(ref, *args) == -1
+
+
+def _gather(h, sizes, chunks=16, lanes=64):
+    fn = h.expert_cache_gather
+    fn.restype = ctypes.c_int
+    fn.argtypes = _lib.SIGNATURES["expert_cache_gather"]
+    args = []
+    for b in sizes:
+        args += [P(1), P(1), ctypes.c_long(b)]
+    return fn(*args, P(1), P(1), chunks, lanes, None)
+
+
+BAD_GATHER = [([16, 16, 16, 16, 16, 0], 16, 64), ([16, 16, 16, 16, 8, 16], 16, 64),
+              ([-16, 16, 16, 16, 16, 16], 16, 64), ([17, 16, 16, 16, 16, 16], 16, 64),
+              ([16] * 6, 0, 64), ([16] * 6, 16, 0), ([16] * 6, -1, 64)]
+
+
+@pytest.mark.parametrize("sizes,chunks,lanes", BAD_GATHER)
+def test_gather_rejects_like_reference(lib, ref, sizes, chunks, lanes):
+    assert _gather(lib, sizes, chunks, lanes) == -1
+    assert _gather(ref, sizes, chunks, lanes) == -1
+
+
+def _fused(h, E, S, mi, bs, L, NB, mk=1):
+    fn = h.expert_cache_fused
+    fn.restype = ctypes.c_int
+    fn.argtypes = _lib.SIGNATURES["expert_cache_fused"]
+    return fn(P(1), mk, E, S, 1, mi, *([P(1)] * 8), bs, L, NB, *([P(1)] * 6), None)
+
+
+BAD_FUSED = [(0, 4, 4, 16, 16, 1), (1025, 4, 4, 16, 16, 1), (8, 0, 4, 16, 16, 1),
+             (8, 1025, 4, 16, 16, 1), (8, 4, -1, 16, 16, 1), (8, 4, 1025, 16, 16, 1),
+             (8, 4, 4, 0, 16, 1), (8, 4, 4, 16, 0, 1), (8, 4, 4, 16, 16, 0)]
+
+
+@pytest.mark.parametrize("args", BAD_FUSED)
+def test_fused_rejects_like_reference(lib, ref, args):
+    assert _fused(lib, *args) == -1
+    assert _fused(ref, *args) == -1
+    assert _fused(lib, 8, 4, 4, 16, 16, 1, mk=-1) == _fused(ref, 8, 4, 4, 16, 16, 1, mk=-1)
+
+
+def test_manage_remap_rejects(lib):
+    fn = lib.expert_cache_manage_remap
+    base = dict(id_bytes=4, E=8, S=4, mi=4, pol=0)
+    for k, v in (("id_bytes", 2), ("id_bytes", 16), ("E", 0), ("S", 0), ("S", 1025),
+                 ("mi", -1), ("mi", 1025), ("pol", 3)):
+        a = dict(base, **{k: v})
+        assert fn(P(1), a["id_bytes"], 1, a["E"], a["S"], 1, a["mi"], *([P(1)] * 8), a["pol"],
+                  64, P(1), None) == -1, (k, v)
+
+
+def test_remap_rejects_and_empty_is_a_no_op(lib):
+    fn = lib.expert_cache_remap
+    assert fn(P(1), 4, 4, P(1), 0, P(1), None) == -1   # E <= 0
+    assert fn(P(1), -1, 4, P(1), 8, P(1), None) == -1  # n < 0
+    assert fn(P(1), 4, 3, P(1), 8, P(1), None) == -1   # id_bytes not 4 or 8
+    assert fn(None, 0, 4, P(1), 8, None, None) == 0    # nothing to do, no launch

@@ -1,0 +1,196 @@
+// libexpertcache.so: C-ABI entry points (declared in include/expert_cache.h).
+//
+// Argument checks run on the host before any HIP call and return -1, exactly where the
+// reference's C-ABI does (kernels/expert_cache.hip:596-598, :616-618, :631-634); otherwise
+// each entry point launches one kernel on the caller's stream and returns hipGetLastError().
+// The library keeps no state and allocates nothing.
+#include <hip/hip_runtime.h>
+
+#include "../../include/expert_cache.h"
+#include "align.h"
+#include "gather.h"
+#include "manage.h"
+
+namespace ec {
+namespace {
+
+// Gather tile: 256 lanes x 8 vectors = 32 KB per workgroup iteration, loads non-temporal
+// (host rows are streamed once), stores default so the fresh slot stays in cache for the
+// GEMM that reads it next.
+constexpr int kGatherUnroll = 8;
+
+bool manage_args_bad(int E, int S, int max_inserts, int policy) {
+  if (E <= 0 || S <= 0 || S > kMaxSlots || S > kSlotMask) return true;
+  if (max_inserts < 0 || max_inserts > kMaxInserts) return true;
+  if (policy < 0 || policy > 1) return true;
+  return false;
+}
+
+template <int IDB, bool REMAP>
+int launch_manage(const ManageArgs& a, hipStream_t stream) {
+  const dim3 grid(1), block(kWave);
+  if (a.E > kLdsExperts) {
+    hipLaunchKernelGGL((manage_k<16, true, IDB, REMAP>), grid, block, 0, stream, a);
+  } else if (a.S <= 64) {
+    hipLaunchKernelGGL((manage_k<1, false, IDB, REMAP>), grid, block, 0, stream, a);
+  } else if (a.S <= 128) {
+    hipLaunchKernelGGL((manage_k<2, false, IDB, REMAP>), grid, block, 0, stream, a);
+  } else if (a.S <= 256) {
+    hipLaunchKernelGGL((manage_k<4, false, IDB, REMAP>), grid, block, 0, stream, a);
+  } else if (a.S <= 512) {
+    hipLaunchKernelGGL((manage_k<8, false, IDB, REMAP>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((manage_k<16, false, IDB, REMAP>), grid, block, 0, stream, a);
+  }
+  return (int)hipGetLastError();
+}
+
+int launch_fused(const ManageArgs& a, const AlignArgs& g, hipStream_t stream) {
+  const dim3 grid(1), block(kWave);
+  if (a.S <= 64)
+    hipLaunchKernelGGL((fused_k<1>), grid, block, 0, stream, a, g);
+  else if (a.S <= 128)
+    hipLaunchKernelGGL((fused_k<2>), grid, block, 0, stream, a, g);
+  else if (a.S <= 256)
+    hipLaunchKernelGGL((fused_k<4>), grid, block, 0, stream, a, g);
+  else if (a.S <= 512)
+    hipLaunchKernelGGL((fused_k<8>), grid, block, 0, stream, a, g);
+  else
+    hipLaunchKernelGGL((fused_k<16>), grid, block, 0, stream, a, g);
+  return (int)hipGetLastError();
+}
+
+ManageArgs make_args(const void* ids, int mk, int E, int S, int max_distinct, int max_inserts,
+                     int* table, int* map_cold, int* slot_expert, long long* slot_stamp,
+                     unsigned char* routed, long long* step, int* miss, int* n_miss,
+                     int policy, int decay, void* out) {
+  ManageArgs a;
+  a.ids = ids;
+  a.mk = mk;
+  a.E = E;
+  a.S = S;
+  a.max_distinct = max_distinct;
+  a.max_inserts = max_inserts;
+  a.table = table;
+  a.map_cold = map_cold;
+  a.slot_expert = slot_expert;
+  a.slot_stamp = slot_stamp;
+  a.routed = routed;
+  a.step = step;
+  a.miss = miss;
+  a.n_miss = n_miss;
+  a.policy = policy;
+  a.decay = decay;
+  a.out = out;
+  return a;
+}
+
+}  // namespace
+}  // namespace ec
+
+using namespace ec;
+
+extern "C" {
+
+int expert_cache_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                        int max_inserts, int* table, int* map_cold, int* slot_expert,
+                        long long* slot_stamp, unsigned char* routed, long long* step,
+                        int* miss, int* n_miss, int policy, int decay, hipStream_t stream) {
+  if (manage_args_bad(E, S, max_inserts, policy)) return -1;
+  const ManageArgs a = make_args(topk_ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                 slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
+                                 decay, nullptr);
+  return launch_manage<4, false>(a, stream);
+}
+
+int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int S,
+                              int max_distinct, int max_inserts, int* table, int* map_cold,
+                              int* slot_expert, long long* slot_stamp, unsigned char* routed,
+                              long long* step, int* miss, int* n_miss, int policy, int decay,
+                              void* out, hipStream_t stream) {
+  if (manage_args_bad(E, S, max_inserts, policy)) return -1;
+  if (id_bytes != 4 && id_bytes != 8) return -1;
+  const ManageArgs a = make_args(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                 slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
+                                 decay, out);
+  return id_bytes == 8 ? launch_manage<8, true>(a, stream) : launch_manage<4, true>(a, stream);
+}
+
+int expert_cache_remap(const void* ids, int n, int id_bytes, const int* table, int E,
+                       void* out, hipStream_t stream) {
+  if (E <= 0 || n < 0 || (id_bytes != 4 && id_bytes != 8)) return -1;
+  if (n == 0) return 0;
+  const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  if (id_bytes == 8)
+    hipLaunchKernelGGL((remap_k<8>), dim3(blocks), dim3(256), 0, stream, ids, n, table, E, out);
+  else
+    hipLaunchKernelGGL((remap_k<4>), dim3(blocks), dim3(256), 0, stream, ids, n, table, E, out);
+  return (int)hipGetLastError();
+}
+
+int expert_cache_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                       int max_inserts, int* table, int* map_cold, int* slot_expert,
+                       long long* slot_stamp, unsigned char* routed, long long* step,
+                       int* miss, int* n_miss, int bs, int L, int NB, int* sorted_hot,
+                       int* eids_hot, int* npad_hot, int* sorted_cold, int* eids_cold,
+                       int* npad_cold, hipStream_t stream) {
+  if (E <= 0 || E > kMaxAlignExperts || S <= 0 || S > kMaxSlots || S > kSlotMask) return -1;
+  if (bs <= 0 || L <= 0 || NB <= 0 || mk < 0) return -1;
+  if (max_inserts < 0 || max_inserts > kMaxAlignExperts) return -1;
+  const ManageArgs a = make_args(topk_ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                 slot_expert, slot_stamp, routed, step, miss, n_miss, 0, 0,
+                                 nullptr);
+  AlignArgs g;
+  g.bs = bs;
+  g.L = L;
+  g.NB = NB;
+  g.sorted_hot = sorted_hot;
+  g.eids_hot = eids_hot;
+  g.npad_hot = npad_hot;
+  g.sorted_cold = sorted_cold;
+  g.eids_cold = eids_cold;
+  g.npad_cold = npad_cold;
+  return launch_fused(a, g, stream);
+}
+
+int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, long b1,
+                        void* d2, const void* s2, long b2, void* d3, const void* s3, long b3,
+                        void* d4, const void* s4, long b4, void* d5, const void* s5, long b5,
+                        const int* miss, const int* n_miss, int chunks, int lanes,
+                        hipStream_t stream) {
+  void* const dst[kGatherBufs] = {d0, d1, d2, d3, d4, d5};
+  const void* const src[kGatherBufs] = {s0, s1, s2, s3, s4, s5};
+  const long bytes[kGatherBufs] = {b0, b1, b2, b3, b4, b5};
+  for (int i = 0; i < kGatherBufs; i++)
+    if (bytes[i] <= 0 || bytes[i] % 16) return -1;
+  if (chunks <= 0 || lanes <= 0) return -1;
+
+  // A buffer passed again with the same (dst, src, bytes) -- the caller's padding of a
+  // short buffer list -- would copy the same bytes to the same place; copy it once.
+  constexpr long long kTile = (long long)kGatherThreads * kGatherUnroll;
+  GatherArgs g;
+  g.nbuf = 0;
+  g.tile0[0] = 0;
+  for (int i = 0; i < kGatherBufs; i++) {
+    bool dup = false;
+    for (int k = 0; k < i; k++)
+      dup = dup || (dst[k] == dst[i] && src[k] == src[i] && bytes[k] == bytes[i]);
+    if (dup) continue;
+    const int b = g.nbuf++;
+    g.dst[b] = static_cast<u32x4*>(dst[i]);
+    g.src[b] = static_cast<const u32x4*>(src[i]);
+    g.vec[b] = bytes[i] / 16;
+    g.tile0[b + 1] = g.tile0[b] + (g.vec[b] + kTile - 1) / kTile;
+  }
+  for (int b = g.nbuf; b < kGatherBufs; b++) {
+    g.dst[b] = nullptr;
+    g.src[b] = nullptr;
+    g.vec[b] = 0;
+    g.tile0[b + 1] = g.tile0[b];
+  }
+  hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false>), dim3(chunks, lanes),
+                     dim3(kGatherThreads), 0, stream, g, miss, n_miss);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

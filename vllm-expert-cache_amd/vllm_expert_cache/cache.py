@@ -1,0 +1,156 @@
+"""Per-MoE-layer expert slot cache.
+
+The layer's full expert tensors stay where the offloader put them (host memory the GPU can
+read). This class adds `num_slots` HBM slot buffers per mirrored tensor and the device
+state of the replacement policy. Each served decode step runs, on the current stream:
+
+  1. expert_cache_manage_remap: marks the routed experts, refreshes their priority, evicts
+     the lowest-priority slots this step does not need, installs the missing experts, writes
+     the (expert, slot) miss list, and rewrites the routing ids into slot ids -- one
+     single-wave kernel.
+  2. expert_cache_gather: pulls each missing expert's slabs from host memory into its slot.
+
+The fused-MoE GEMM then runs unchanged against the slot buffers with the slot ids. Nothing
+reads a device value back to the host, so the sequence is graph-capturable, and the kernels
+are deterministic, so tensor-parallel ranks seeing the same routing keep identical caches
+without talking to each other.
+
+Constructor, attributes and methods mirror vllm_expert_cache/cache.py:38-163 of the
+reference (`fits`, `remap`, `refresh`, `slots`, `bound`, `names`, `skipped`, `E`, `S`).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from ._lib import GATHER_SLOTS, lib
+from .config import settings
+
+# Gather grid (workgroups = chunks x lanes, 256 lanes each). The kernel spreads the step's
+# (miss, buffer, tile) work over the whole grid, so the product is what matters: 512
+# workgroups keep every one of an expert's ~150 32-KB tiles in flight at once and leave
+# room for several misses, while a step with no miss still retires quickly.
+DEFAULT_CHUNKS = 32
+DEFAULT_LANES = 16
+
+
+def _bytes_per_expert(t: torch.Tensor) -> int:
+    return (t.numel() // t.shape[0]) * t.element_size()
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class ExpertSlotCache:
+    """Holds `num_slots` of `num_experts` experts resident in device memory."""
+
+    def __init__(self, owner, source_names, num_experts: int, num_slots: int, device,
+                 required=()):
+        # Sources are re-read from `owner` on every step: vLLM's offloader moves expert
+        # tensors to host memory after loading, so a pointer taken now would go stale.
+        self.owner = owner
+        self.names = list(source_names)
+        self.E = int(num_experts)
+        self.S = int(num_slots)
+
+        self.slots: dict[str, torch.Tensor] = {}
+        self.skipped: list[str] = []
+        ragged = []
+        for n in self.names:
+            full = getattr(owner, n).data
+            # The gather moves 16-byte vectors. A ragged weight the GEMM reads directly is
+            # fatal; a ragged auxiliary tensor is left unmirrored and the caller's leak check
+            # decides whether the quantisation config actually indexes it per expert.
+            nbytes = _bytes_per_expert(full)
+            if nbytes % 16:
+                (ragged if n in required else self.skipped).append(
+                    f"{n}{tuple(full.shape)}={nbytes}B")
+                continue
+            self.slots[n] = torch.empty((self.S,) + tuple(full.shape[1:]), dtype=full.dtype,
+                                        device=device)
+        if ragged:
+            raise ValueError("per-expert slab must be a multiple of 16 bytes, but these are "
+                             "not: " + ", ".join(ragged))
+        self.names = [n for n in self.names if n in self.slots]
+
+        # What the layer's attributes are rebound to during a cached step; built once so
+        # graph capture sees fixed storage.
+        self.bound: dict[str, torch.Tensor] = dict(self.slots)
+
+        i32, i64, u8 = torch.int32, torch.int64, torch.uint8
+        self.table = torch.full((self.E,), -1, dtype=i32, device=device)
+        self.map_cold = torch.arange(self.E, dtype=i32, device=device)
+        self.slot_expert = torch.full((self.S,), -1, dtype=i32, device=device)
+        self.slot_stamp = torch.zeros((self.S,), dtype=i64, device=device)
+        self.routed = torch.zeros((self.E,), dtype=u8, device=device)
+        self.step = torch.zeros((1,), dtype=i64, device=device)
+        self.miss = torch.zeros((2 * self.S,), dtype=i32, device=device)
+        self.n_miss = torch.zeros((1,), dtype=i32, device=device)
+
+        self.policy = settings.policy_code
+        self.decay = settings.decay
+        self.chunks = int(os.environ.get("EXPERT_CACHE_CHUNKS", str(DEFAULT_CHUNKS)))
+        self.lanes = int(os.environ.get("EXPERT_CACHE_LANES", str(DEFAULT_LANES)))
+
+    def fits(self, topk_ids: torch.Tensor) -> bool:
+        """Can this step be served from slots? tokens x top_k bounds the distinct experts
+        the step touches; it is shape metadata, so deciding costs no device sync."""
+        return topk_ids.numel() <= self.S
+
+    @staticmethod
+    def _id_view(topk_ids: torch.Tensor) -> tuple[torch.Tensor, int]:
+        if topk_ids.dtype == torch.int32:
+            return topk_ids.contiguous(), 4
+        if topk_ids.dtype == torch.int64:
+            return topk_ids.contiguous(), 8
+        return topk_ids.to(torch.int32).contiguous(), 4
+
+    def _stream(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(self.table.device).cuda_stream)
+
+    def remap(self, topk_ids: torch.Tensor) -> torch.Tensor:
+        """Routing ids rewritten as slot ids against the current table (negative ids wrap
+        as torch indexing does). Valid after `refresh`."""
+        ids, nbytes = self._id_view(topk_ids)
+        out = torch.empty_like(ids)
+        rc = lib().expert_cache_remap(_ptr(ids), int(ids.numel()), nbytes, _ptr(self.table),
+                                      self.E, _ptr(out), self._stream())
+        if rc != 0:
+            raise RuntimeError(f"expert_cache_remap failed rc={rc}")
+        return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
+
+    def refresh(self, topk_ids: torch.Tensor) -> torch.Tensor:
+        """Run the policy step and the gather for this step; return slot-space ids."""
+        h = lib()
+        stream = self._stream()
+        ids, nbytes = self._id_view(topk_ids)
+        out = torch.empty_like(ids)
+        mk = int(ids.numel())
+
+        rc = h.expert_cache_manage_remap(
+            _ptr(ids), nbytes, mk, self.E, self.S, min(self.E, mk), self.S,
+            _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
+            _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.step), _ptr(self.miss),
+            _ptr(self.n_miss), self.policy, self.decay, _ptr(out), stream)
+        if rc != 0:
+            raise RuntimeError(f"expert_cache_manage failed rc={rc}")
+
+        dsts = [self.slots[n] for n in self.names]
+        srcs = [getattr(self.owner, n).data for n in self.names]
+        for i in range(0, len(dsts), GATHER_SLOTS):
+            gd, gs = dsts[i:i + GATHER_SLOTS], srcs[i:i + GATHER_SLOTS]
+            while len(gd) < GATHER_SLOTS:  # pad with a repeat; the library copies it once
+                gd.append(gd[-1])
+                gs.append(gs[-1])
+            args = []
+            for d, s in zip(gd, gs):
+                args += [_ptr(d), _ptr(s), ctypes.c_long(_bytes_per_expert(s))]
+            rc = h.expert_cache_gather(*args, _ptr(self.miss), _ptr(self.n_miss),
+                                       self.chunks, self.lanes, stream)
+            if rc != 0:
+                raise RuntimeError(f"expert_cache_gather failed rc={rc}")
+
+        return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
