@@ -99,7 +99,7 @@ def main():
     import torch
 
     from vllm_expert_cache import _lib, traces
-    from vllm_expert_cache.cache import DEFAULT_CHUNKS, DEFAULT_LANES
+    from vllm_expert_cache.cache import DEFAULT_CHUNKS, DEFAULT_LANES, device_address
 
     lib = _lib.lib()  # raises if the HIP library is missing: there is no fallback
     dev = torch.device("cuda:0")
@@ -122,6 +122,8 @@ def main():
     host = []  # host[l][b]: pinned [E * bytes_b]
     for l in range(L):
         host.append([torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs])
+        if l % 8 == 7:
+            log(f"  pinned host store: {l + 1}/{L} layers, {time.time() - t0:.1f}s")
     slots = [[torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
              for _ in range(L)]
     log(f"setup: routing {ids_np.shape}, host store {L * E * B_exp / 1e9:.1f} GB pinned, "
@@ -141,7 +143,7 @@ def main():
         for i in range(6):  # pad to six buffers with a repeat, as cache.refresh does
             j = min(i, len(bufs) - 1)
             a += [ctypes.c_void_p(slots[l][j].data_ptr()),
-                  ctypes.c_void_p(host[l][j].data_ptr()), ctypes.c_long(bufs[j])]
+                  ctypes.c_void_p(device_address(host[l][j])), ctypes.c_long(bufs[j])]
         return a
 
     def manage_args(l, ids_p, nm_p, out_p):
@@ -266,7 +268,7 @@ def main():
     memcpy_gbps = 5 * n_peak / (a.elapsed_time(b) * 1e-3) / 1e9
     one = torch.tensor([0, 0], dtype=torch.int32, device=dev)
     one_n = torch.tensor([1], dtype=torch.int32, device=dev)
-    big = [ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+    big = [ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(device_address(src)),
            ctypes.c_long(n_peak)] * 6
     tail = (ctypes.c_void_p(one.data_ptr()), ctypes.c_void_p(one_n.data_ptr()), chunks, lanes,
             s_ptr)

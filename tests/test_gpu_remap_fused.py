@@ -118,7 +118,7 @@ def test_fused_wide_step_is_token_ordered():
         a = o_r[f"sorted_{side}"].cpu().numpy()
         b = outs[f"sorted_{side}"].cpu().numpy()
         e = outs[f"eids_{side}"].cpu().numpy()
-        for blk in range(NB):               # same multiset per block
-            sl = slice(blk * bs, (blk + 1) * bs)
-            if e[blk] >= 0:
-                assert sorted(a[sl].tolist()) == sorted(b[sl].tolist()), (side, blk)
+        for bucket in np.unique(e[e >= 0]):  # same ids per bucket, in any order
+            blocks = np.nonzero(e == bucket)[0]
+            sl = slice(blocks[0] * bs, (blocks[-1] + 1) * bs)
+            assert sorted(a[sl].tolist()) == sorted(b[sl].tolist()), (side, bucket)

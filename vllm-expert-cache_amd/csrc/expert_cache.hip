@@ -14,10 +14,14 @@
 namespace ec {
 namespace {
 
-// Gather tile: 256 lanes x 8 vectors = 32 KB per workgroup iteration, loads non-temporal
+// Gather tile: 256 lanes x 2 vectors = 8 KB per workgroup iteration, loads non-temporal
 // (host rows are streamed once), stores default so the fresh slot stays in cache for the
-// GEMM that reads it next.
-constexpr int kGatherUnroll = 8;
+// GEMM that reads it next. Measured on MI355X over PCIe Gen5: the host link saturates at
+// ~128-256 KB in flight (its bandwidth-delay product); far more in flight at once (every
+// tile of an expert issued together) drops a 4.7 MB expert from ~54.5 to ~41 GB/s. So the
+// caller's grid should be small (32 workgroups x 8 KB = 256 KB) and the tiles stream
+// through the expert in order, each workgroup taking every grid-th tile.
+constexpr int kGatherUnroll = 2;
 
 bool manage_args_bad(int E, int S, int max_inserts, int policy) {
   if (E <= 0 || S <= 0 || S > kMaxSlots || S > kSlotMask) return true;

@@ -4,9 +4,10 @@
 //
 // The work is flattened instead of split by miss: one miss is `per_miss` tiles (each buffer
 // cut into tiles of 256 lanes x U 16-byte vectors), and tile t of the whole step goes to
-// workgroup t mod grid. One ~4.7 MB expert is ~150 tiles of 32 KB, so a single miss already
-// spreads over ~150 CUs with every lane holding U loads in flight -- the host link, not the
-// number of active CUs, is what bounds it. The grid shape is fixed at launch and the tile
+// workgroup t mod grid, so the grid's loads form one front that streams through the miss
+// list in address order whatever n_miss is. What bounds the copy is the host link, and it
+// is saturated by a modest amount of data in flight (grid x tile, ~256 KB); the grid is
+// sized for that, not for the CU count. The grid shape is fixed at launch and the tile
 // count is read from n_miss on the device, so the launch stays graph-capturable.
 #pragma once
 #include <hip/hip_runtime.h>

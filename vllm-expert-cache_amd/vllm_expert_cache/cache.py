@@ -28,12 +28,13 @@ import torch
 from ._lib import GATHER_SLOTS, lib
 from .config import settings
 
-# Gather grid (workgroups = chunks x lanes, 256 lanes each). The kernel spreads the step's
-# (miss, buffer, tile) work over the whole grid, so the product is what matters: 512
-# workgroups keep every one of an expert's ~150 32-KB tiles in flight at once and leave
-# room for several misses, while a step with no miss still retires quickly.
+# Gather grid: chunks x lanes workgroups of 256 lanes, each holding one 8-KB tile of loads
+# in flight. The kernel spreads the step's (miss, buffer, tile) work over the whole grid,
+# so only the product matters. On MI355X the host link is saturated by ~128-256 KB in
+# flight and degrades with much more (measured: 32 workgroups reach ~54.5 GB/s on one
+# 4.7 MB expert, 512 reach ~41 GB/s), hence 32 x 1 rather than the reference's 16 x 64.
 DEFAULT_CHUNKS = 32
-DEFAULT_LANES = 16
+DEFAULT_LANES = 1
 
 
 def _bytes_per_expert(t: torch.Tensor) -> int:
@@ -42,6 +43,29 @@ def _bytes_per_expert(t: torch.Tensor) -> int:
 
 def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
+
+
+_HIP = None
+
+
+def device_address(t: torch.Tensor) -> int:
+    """Address at which the GPU reads `t`: its own for a device tensor (vLLM's offloader
+    hands over device views of host memory), or the device mapping of page-locked host
+    memory from hipHostGetDevicePointer for a pinned CPU tensor."""
+    if t.is_cuda:
+        return t.data_ptr()
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+        _HIP.hipHostGetDevicePointer.restype = ctypes.c_int
+        _HIP.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p),
+                                                 ctypes.c_void_p, ctypes.c_uint]
+    out = ctypes.c_void_p()
+    rc = _HIP.hipHostGetDevicePointer(ctypes.byref(out), ctypes.c_void_p(t.data_ptr()), 0)
+    if rc != 0 or not out.value:
+        raise ValueError(f"expert source at {t.data_ptr():#x} is host memory the GPU cannot "
+                         f"read (hipHostGetDevicePointer rc={rc}); pin it")
+    return out.value
 
 
 class ExpertSlotCache:
@@ -147,7 +171,8 @@ class ExpertSlotCache:
                 gs.append(gs[-1])
             args = []
             for d, s in zip(gd, gs):
-                args += [_ptr(d), _ptr(s), ctypes.c_long(_bytes_per_expert(s))]
+                args += [_ptr(d), ctypes.c_void_p(device_address(s)),
+                         ctypes.c_long(_bytes_per_expert(s))]
             rc = h.expert_cache_gather(*args, _ptr(self.miss), _ptr(self.n_miss),
                                        self.chunks, self.lanes, stream)
             if rc != 0:
