@@ -51,13 +51,55 @@ def parse():
     p.add_argument("--slots", type=int, default=64)
     p.add_argument("--policy", choices=("lfu", "lru"), default="lfu")
     p.add_argument("--layers", type=int, default=48)
-    p.add_argument("--timing-window", type=int, default=32,
-                   help="timed steps re-run with per-kernel HIP events")
+    p.add_argument("--timing-segments", type=int, default=8,
+                   help="segments of the timed steps re-run with per-kernel HIP events")
+    p.add_argument("--segment-steps", type=int, default=8)
     p.add_argument("--cpu-steps", type=int, default=512,
                    help="timed steps in the CPU-baseline sample (0 to skip)")
     p.add_argument("--chunks", type=int, default=None)
     p.add_argument("--lanes", type=int, default=None)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="for rocprofv3 --pmc runs: 16 gathers of one expert each and 8 plain "
+                        "device copies of 64 MiB (the counter calibration), nothing else")
     return p.parse_args()
+
+
+def traffic_probe(args):
+    """Known work for the FETCH_SIZE / WRITE_SIZE counter runs: the counter value of the
+    plain copy per byte calibrates the gather's per-launch counter into bytes."""
+    import torch
+
+    from vllm_expert_cache import _lib, traces
+    from vllm_expert_cache.cache import DEFAULT_CHUNKS, DEFAULT_LANES, device_address
+
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    w = traces.WORKLOADS[WORKLOAD]
+    E, S = w.experts, args.slots
+    bufs = [b.nbytes for b in w.buffers]
+    host = [torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs]
+    slots = [torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
+    a = []
+    for i in range(6):
+        j = min(i, len(bufs) - 1)
+        a += [ctypes.c_void_p(slots[j].data_ptr()), ctypes.c_void_p(device_address(host[j])),
+              ctypes.c_long(bufs[j])]
+    miss = torch.tensor([[e, e % S] for e in range(16)], dtype=torch.int32, device=dev)
+    one = torch.ones(1, dtype=torch.int32, device=dev)
+    s_ptr = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for r in range(16):
+        rc = lib.expert_cache_gather(*a, ctypes.c_void_p(miss[r].data_ptr()),
+                                     ctypes.c_void_p(one.data_ptr()), args.chunks or
+                                     DEFAULT_CHUNKS, args.lanes or DEFAULT_LANES, s_ptr)
+        assert rc == 0
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"gather_launches": 16, "gather_bytes_per_launch": sum(bufs),
+                      "copy_launches": 8, "copy_bytes_per_launch": n}), flush=True)
 
 
 class Layers:
@@ -89,6 +131,9 @@ class Layers:
 
 def main():
     args = parse()
+    if args.traffic_probe:
+        traffic_probe(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no cross-GPU work (each tensor-"
               f"parallel rank runs its own identical cache); --gpus {args.gpus} is not "
@@ -179,21 +224,29 @@ def main():
         launch_step(torch.cuda.current_stream())
     torch.cuda.synchronize()
 
-    def run_steps(t_from, t_to):
+    def run_steps(t_from, t_to, snaps=None):
         for t in range(t_from, t_to):
+            if snaps is not None and t in snaps:
+                for f in st.fields:
+                    snaps[t][f].copy_(getattr(st, f), non_blocking=True)
             ids_static.copy_(ids_dev[t], non_blocking=True)
             graph.replay()
             nm_hist[t].copy_(nm_static, non_blocking=True)
 
     # ---- warm-up, then the timed steps -----------------------------------------------------
+    # state snapshots at the start of the segments that are re-run with per-kernel events
+    nseg = max(1, min(args.timing_segments, K))
+    seg_len = max(1, min(args.segment_steps, K // nseg))
+    seg_starts = [W + (k * (K - seg_len)) // max(1, nseg - 1) for k in range(nseg)] \
+        if nseg > 1 else [W]
+    snaps = {t: st.snapshot() for t in seg_starts}
     run_steps(0, W)
     torch.cuda.synchronize()
-    snap = st.snapshot()
     ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     ev_a.record()
-    run_steps(W, T)
+    run_steps(W, T, snaps)
     ev_b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
@@ -207,46 +260,51 @@ def main():
     log(f"timed: {K} steps in {elapsed_s:.2f}s ({1e3 * elapsed_s / K:.3f} ms/step), "
         f"{inserts} inserts, {gathered / 1e9:.1f} GB -> {value:.2f} GB/s")
 
-    # ---- per-kernel durations: a window of the timed steps, HIP events per launch ---------
+    # ---- per-kernel durations: segments of the timed steps re-run from their snapshots, --
+    # ---- HIP events around every launch on the launch stream ----------------------------
     final = st.snapshot()
-    st.restore(snap)
-    win = max(1, min(args.timing_window, K))
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(win)]
     stream = torch.cuda.current_stream()
     s_ptr = ctypes.c_void_p(stream.cuda_stream)
-    win_out = torch.zeros((win, L, mk), dtype=torch.int32, device=dev)
-    win_nm = torch.zeros((win, L), dtype=torch.int32, device=dev)
-    torch.cuda.synchronize()
-    torch.cuda._sleep(int(5e8))  # hold the stream while the window is queued behind it
-    for i in range(win):
-        t = W + i
-        for l in range(L):
-            e0, e1, e2 = ev[i][l]
-            e0.record(stream)
-            rc = lib.expert_cache_manage_remap(
-                *manage_args(l, row(ids_dev[t], l), row(win_nm[i], l), row(win_out[i], l)),
-                s_ptr)
-            e1.record(stream)
-            rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
-                                          row(win_nm[i], l), chunks, lanes, s_ptr)
-            e2.record(stream)
-            if rc:
-                raise RuntimeError(f"launch failed rc={rc}")
-    torch.cuda.synchronize()
-    man_us = np.array([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
-                       for i in range(win)])
-    gat_us = np.array([[ev[i][l][1].elapsed_time(ev[i][l][2]) * 1e3 for l in range(L)]
-                       for i in range(win)])
-    wnm = win_nm.cpu().numpy()
-    assert np.array_equal(wnm, nm[W:W + win]), "window replay diverged from the timed steps"
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(seg_len)]
+    seg_out = torch.zeros((seg_len, L, mk), dtype=torch.int32, device=dev)
+    seg_nm = torch.zeros((seg_len, L), dtype=torch.int32, device=dev)
+    man_us, gat_us, wnm = [], [], []
+    for t0s in seg_starts:
+        st.restore(snaps[t0s])
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(2e8))  # hold the stream while the segment is queued behind it
+        for i in range(seg_len):
+            t = t0s + i
+            for l in range(L):
+                e0, e1, e2 = ev[i][l]
+                e0.record(stream)
+                rc = lib.expert_cache_manage_remap(
+                    *manage_args(l, row(ids_dev[t], l), row(seg_nm[i], l), row(seg_out[i], l)),
+                    s_ptr)
+                e1.record(stream)
+                rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
+                                              row(seg_nm[i], l), chunks, lanes, s_ptr)
+                e2.record(stream)
+                if rc:
+                    raise RuntimeError(f"launch failed rc={rc}")
+        torch.cuda.synchronize()
+        man_us.append([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
+                       for i in range(seg_len)])
+        gat_us.append([[ev[i][l][1].elapsed_time(ev[i][l][2]) * 1e3 for l in range(L)]
+                       for i in range(seg_len)])
+        got = seg_nm.cpu().numpy()
+        assert np.array_equal(got, nm[t0s:t0s + seg_len]), "segment diverged from timed run"
+        wnm.append(got)
     st.restore(final)
+    man_us, gat_us, wnm = np.array(man_us), np.array(gat_us), np.array(wnm)
+    win = nseg * seg_len
     miss_launch = wnm > 0
     win_bytes = wnm.sum() * B_exp
     achieved = win_bytes / (gat_us.sum() * 1e-6) / 1e9
     per_miss = (wnm[miss_launch].sum() * B_exp / (gat_us[miss_launch].sum() * 1e-6) / 1e9
                 if miss_launch.any() else None)
-    log(f"window {win} steps: manage+remap {man_us.mean():.2f} us/layer "
+    log(f"{nseg} segments x {seg_len} steps: manage+remap {man_us.mean():.2f} us/layer "
         f"(p50 {np.median(man_us):.2f}), gather {gat_us.mean():.1f} us/launch, "
         f"{achieved:.2f} GB/s over all launches, {per_miss} GB/s over launches with a miss, "
         f"{gat_us[~miss_launch].mean() if (~miss_launch).any() else float('nan'):.2f} us "
@@ -288,7 +346,7 @@ def main():
     # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer) --------------
     cpu = None
     if args.cpu_steps > 0:
-        cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk,
+        cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
                            policy, decay, W, dev)
 
     res = {
@@ -318,9 +376,10 @@ def main():
                            "gather_kernel_256MB": round(kernel_gbps, 3)},
         "roofline": {"bound": "host-link", "kernel": "gather_k", "achieved": round(achieved, 3),
                      "peak": round(peak, 3), "unit": "GB/s", "frac": round(achieved / peak, 4),
-                     "traffic": None,
-                     "achieved_def": f"gathered bytes / summed gather kernel time, {win} "
-                                     f"timed steps x {L} layers, HIP events",
+                     "traffic": _traffic(),
+                     "achieved_def": f"gathered bytes / summed gather kernel time, {nseg} "
+                                     f"segments x {seg_len} of the timed steps x {L} layers, "
+                                     f"HIP events around each launch",
                      "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
                                  "kernel on one 256 MB slab)"},
         "cpu_baseline": cpu,
@@ -386,6 +445,21 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
             "policy_us_per_layer_step": round(policy_us, 4),
             "host_memcpy_GBps": round(host_memcpy, 2),
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _traffic():
+    """Measured bytes per one-miss gather launch (rocprofv3 FETCH_SIZE / WRITE_SIZE,
+    calibrated on a plain copy), from the committed profile summary; None if absent."""
+    p = ROOT / "profiles" / "gather_k-traffic-48-layer-e128.json"
+    try:
+        t = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    return {"fetch_bytes_per_miss": t["fetch_bytes_per_launch"],
+            "write_bytes_per_miss": t["write_bytes_per_launch"],
+            "algorithmic_bytes_per_miss": t["algorithmic_bytes_per_launch"],
+            "fetch_over_algorithmic": t["fetch_over_algorithmic"],
+            "source": f"profiles/{p.name}"}
 
 
 def _cpu_model():
