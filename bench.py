@@ -37,6 +37,11 @@ sys.path.insert(0, str(ROOT / "vllm-expert-cache_amd"))
 
 METRIC = ("host->HBM gather GB/s (% link peak); manage+remap µs/layer; hit rate")
 WORKLOAD = "48-layer-e128"
+# slot budget each workload is measured at by default, and a cap on its timed steps where
+# one step moves gigabytes
+TARGET_SLOTS = {"single-layer-e128": 64, "48-layer-e128": 64, "48-layer-e128-batch4": 48,
+                "8-layer-e8-bf16": 4, "8-layer-e256-fp8": 128}
+MAX_STEPS = {"8-layer-e256-fp8": 64}
 
 
 def log(*a):
@@ -46,11 +51,18 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=4032)
+    p.add_argument("--workload", default=WORKLOAD,
+                   help="48-layer-e128 (default), 48-layer-e128-batch4, 8-layer-e8-bf16, "
+                        "8-layer-e256-fp8, single-layer-e128")
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed steps (default: the rest of the workload's trace)")
     p.add_argument("--warmup", type=int, default=64)
-    p.add_argument("--slots", type=int, default=64)
+    p.add_argument("--slots", type=int, default=None,
+                   help="slot budget (default: the workload's target budget)")
     p.add_argument("--policy", choices=("lfu", "lru"), default="lfu")
-    p.add_argument("--layers", type=int, default=48)
+    p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--no-hit-sweep", action="store_true",
+                   help="skip the per-budget, per-policy hit-rate pass over the whole trace")
     p.add_argument("--timing-segments", type=int, default=8,
                    help="segments of the timed steps re-run with per-kernel HIP events")
     p.add_argument("--segment-steps", type=int, default=8)
@@ -75,7 +87,7 @@ def traffic_probe(args):
     lib = _lib.lib()
     dev = torch.device("cuda:0")
     w = traces.WORKLOADS[WORKLOAD]
-    E, S = w.experts, args.slots
+    E, S = w.experts, args.slots or TARGET_SLOTS[WORKLOAD]
     bufs = [b.nbytes for b in w.buffers]
     host = [torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs]
     slots = [torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
@@ -149,13 +161,19 @@ def main():
     lib = _lib.lib()  # raises if the HIP library is missing: there is no fallback
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    w = traces.WORKLOADS[WORKLOAD]
-    L, E, S, mk = args.layers, w.experts, args.slots, w.mk
+    w = traces.WORKLOADS[args.workload]
+    L = args.layers or w.layers
+    E, mk = w.experts, w.mk
+    S = args.slots or TARGET_SLOTS[w.name]
+    if mk > S:
+        raise SystemExit(f"{w.name}: {mk} routing ids per step exceed {S} slots, so every step "
+                         f"reads through and there is nothing to time; pick --slots >= {mk}")
     policy = 1 if args.policy == "lfu" else 0
     decay = 64
     chunks = args.chunks or DEFAULT_CHUNKS
     lanes = args.lanes or DEFAULT_LANES
-    W, K = args.warmup, args.steps
+    W = min(args.warmup, w.steps - 1)
+    K = args.steps or min(w.steps - W, MAX_STEPS.get(w.name, w.steps))
     T = W + K
     bufs = [b.nbytes for b in w.buffers]
     B_exp = sum(bufs)
@@ -165,10 +183,23 @@ def main():
     ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)  # [T, L, mk]
     ids_dev = torch.as_tensor(ids_np, device=dev)
     host = []  # host[l][b]: pinned [E * bytes_b]
-    for l in range(L):
-        host.append([torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs])
-        if l % 8 == 7:
-            log(f"  pinned host store: {l + 1}/{L} layers, {time.time() - t0:.1f}s")
+    host_store = "per layer"
+    try:
+        for l in range(L):
+            host.append([torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs])
+            if l % 8 == 7:
+                log(f"  pinned host store: {l + 1}/{L} layers, {time.time() - t0:.1f}s")
+    except (RuntimeError, torch.AcceleratorError) as exc:
+        # this host cannot pin one store per layer: every layer reads one shared store, which
+        # moves the same bytes per miss from the same kind of memory
+        log(f"  pinning {L * E * B_exp / 1e9:.1f} GB failed ({type(exc).__name__}); layers "
+            f"share one {E * B_exp / 1e9:.1f} GB store")
+        host = []
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        shared = [torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs]
+        host = [shared] * L
+        host_store = f"shared by all layers (pinning {L * E * B_exp / 1e9:.1f} GB failed)"
     slots = [[torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
              for _ in range(L)]
     log(f"setup: routing {ids_np.shape}, host store {L * E * B_exp / 1e9:.1f} GB pinned, "
@@ -349,6 +380,10 @@ def main():
         cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
                            policy, decay, W, dev)
 
+    sweep = None
+    if not args.no_hit_sweep:
+        sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
+
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -362,10 +397,11 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic",
-        "config": {"workload": WORKLOAD, "layers": L, "experts": E, "top_k": w.top_k,
+        "config": {"workload": w.name, "layers": L, "experts": E, "top_k": w.top_k,
                    "tokens_per_step": w.tokens, "slots": S, "policy": args.policy,
                    "decay": decay, "bytes_per_expert": B_exp, "host_store_GB":
-                   round(L * E * B_exp / 1e9, 2), "gather_grid": [chunks, lanes],
+                   round(L * E * B_exp / 1e9, 2), "host_store": host_store,
+                   "gather_grid": [chunks, lanes],
                    "timed_trace_steps": [W, T]},
         "hit_rate": round(1.0 - inserts / distinct, 5),
         "inserts": inserts,
@@ -383,6 +419,7 @@ def main():
                      "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
                                  "kernel on one 256 MB slab)"},
         "cpu_baseline": cpu,
+        "hit_rate_sweep": sweep,
     }
     print(json.dumps(res), flush=True)
 
@@ -445,6 +482,79 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
             "policy_us_per_layer_step": round(policy_us, 4),
             "host_memcpy_GBps": round(host_memcpy, 2),
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _row(t, l):
+    return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
+
+
+def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
+    """Hit rate per slot budget and policy over the whole trace from a cold start, on the
+    GPU policy kernel: one captured graph of L manage+remap launches per step (no gather;
+    hit rate and gather volume depend only on the policy). Also the graph's time per layer,
+    which is kernel time plus graph node gaps plus the per-step id copy."""
+    T = ids_np.shape[0]
+    srt = np.sort(ids_np, axis=-1)
+    distinct = 1 + (np.diff(srt, axis=-1) != 0).sum(-1)  # [T, L]
+    out = []
+    for S in w.slots:
+        if mk > S:
+            out.append({"slots": S, "served_steps": 0,
+                        "note": "tokens x top_k > slots: every step reads through"})
+            continue
+        for pol_name in w.policies:
+            pol = 1 if pol_name == "lfu" else 0
+            st = Layers(torch, L, E, S, dev)
+            snap0 = st.snapshot()
+            ids_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+            out_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+            nm_static = torch.zeros((L,), dtype=torch.int32, device=dev)
+            nm_hist = torch.zeros((T, L), dtype=torch.int32, device=dev)
+            args_l = [(_row(ids_static, l), 4, mk, E, S, min(E, mk), S, st.row("table", l),
+                       st.row("map_cold", l), st.row("slot_expert", l),
+                       st.row("slot_stamp", l), st.row("routed", l), st.row("step", l),
+                       st.row("miss", l), _row(nm_static, l), pol, decay, _row(out_static, l))
+                      for l in range(L)]
+
+            def launch(stream):
+                sp = ctypes.c_void_p(stream.cuda_stream)
+                for l in range(L):
+                    if lib.expert_cache_manage_remap(*args_l[l], sp):
+                        raise RuntimeError("manage launch failed")
+
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                launch(side)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            st.restore(snap0)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                launch(torch.cuda.current_stream())
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for t in range(T):
+                ids_static.copy_(ids_dev[t], non_blocking=True)
+                g.replay()
+                nm_hist[t].copy_(nm_static, non_blocking=True)
+            b.record()
+            torch.cuda.synchronize()
+            nm = nm_hist.cpu().numpy()
+            per_layer = 1.0 - nm.sum(0) / distinct.sum(0)
+            out.append({"slots": S, "policy": pol_name, "steps": T,
+                        "hit_rate": round(float(1.0 - nm.sum() / distinct.sum()), 5),
+                        "per_layer_hit_rate_min": round(float(per_layer.min()), 5),
+                        "per_layer_hit_rate_max": round(float(per_layer.max()), 5),
+                        "inserts": int(nm.sum()),
+                        "gather_volume_GB": round(float(nm.sum()) * w.bytes_per_expert / 1e9, 2),
+                        "graph_us_per_layer": round(a.elapsed_time(b) * 1e3 / (T * L), 3)})
+            log(f"hit-rate sweep: S={S} {pol_name}: {out[-1]['hit_rate']} "
+                f"(layers {out[-1]['per_layer_hit_rate_min']}..{out[-1]['per_layer_hit_rate_max']}), "
+                f"{out[-1]['gather_volume_GB']} GB, {out[-1]['graph_us_per_layer']} us/layer")
+            del g
+    return out
 
 
 def _traffic():

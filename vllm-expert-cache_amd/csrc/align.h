@@ -124,6 +124,7 @@ template <int CS>
 __global__ __launch_bounds__(kWave) void fused_k(ManageArgs a, AlignArgs g) {
   __shared__ ManageLds<false> L;
   __shared__ AlignLds A;
+  args_in_sgprs(a);
   long long idv[kIdRegs];
   manage_step<CS, false, 4>(a, L, idv);
   lds_sync();

@@ -27,47 +27,102 @@ struct GatherArgs {
   int nbuf;                              // distinct buffers after de-duplication
 };
 
+// Position of one tile: miss j, buffer b, first vector `off`, vectors `n`, and the source and
+// destination of that range.
+struct GatherTile {
+  const u32x4* src;
+  u32x4* dst;
+  int n;
+};
+
+template <int U>
+__device__ __forceinline__ GatherTile gather_tile(const GatherArgs& g, int e, int sl,
+                                                  long long r) {
+  constexpr long long kTile = (long long)kGatherThreads * U;
+  int b = 0;
+  while (b + 1 < g.nbuf && r >= g.tile0[b + 1]) ++b;
+  const long long V = g.vec[b];
+  const long long off = (r - g.tile0[b]) * kTile;
+  GatherTile t;
+  t.src = g.src[b] + (long long)e * V + off;
+  t.dst = g.dst[b] + (long long)sl * V + off;
+  t.n = (int)min(kTile, V - off);
+  return t;
+}
+
+template <int U, bool NT_LOAD>
+__device__ __forceinline__ void tile_load(const GatherTile& t, u32x4 (&v)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + u * kGatherThreads;
+    if (i < t.n) {
+      if constexpr (NT_LOAD)
+        v[u] = __builtin_nontemporal_load(t.src + i);
+      else
+        v[u] = t.src[i];
+    }
+  }
+}
+
+template <int U, bool NT_STORE>
+__device__ __forceinline__ void tile_store(const GatherTile& t, const u32x4 (&v)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + u * kGatherThreads;
+    if (i < t.n) {
+      if constexpr (NT_STORE)
+        __builtin_nontemporal_store(v[u], t.dst + i);
+      else
+        t.dst[i] = v[u];
+    }
+  }
+}
+
+// Each workgroup walks tiles blockId, blockId + grid, ... of the step. The walk keeps its
+// (miss, tile-in-miss) position incrementally (no division per tile), reloads the miss pair
+// only when the walk moves to another miss, and issues the next tile's host loads before
+// storing the current tile, so the scalar bookkeeping never sits between two tiles' loads.
 template <int U, bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
                                                            const int* __restrict__ miss,
                                                            const int* __restrict__ n_miss) {
-  constexpr int kTile = kGatherThreads * U;
-  const long long per_miss = g.tile0[g.nbuf];
-  const long long total = (long long)n_miss[0] * per_miss;
+  const long long per = g.tile0[g.nbuf];
   const long long nblk = (long long)gridDim.x * gridDim.y;
-  for (long long t = (long long)blockIdx.y * gridDim.x + blockIdx.x; t < total; t += nblk) {
-    const int j = (int)(t / per_miss);
-    const long long r = t - (long long)j * per_miss;
-    int b = 0;
-    while (b + 1 < g.nbuf && r >= g.tile0[b + 1]) ++b;
-    const int e = miss[2 * j];
-    const int sl = miss[2 * j + 1];
-    const long long V = g.vec[b];
-    const long long off = (r - g.tile0[b]) * kTile;
-    const int n = (int)min((long long)kTile, V - off);
-    const u32x4* __restrict__ s = g.src[b] + (long long)e * V + off;
-    u32x4* __restrict__ d = g.dst[b] + (long long)sl * V + off;
-    u32x4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = threadIdx.x + u * kGatherThreads;
-      if (i < n) {
-        if constexpr (NT_LOAD)
-          v[u] = __builtin_nontemporal_load(s + i);
-        else
-          v[u] = s[i];
-      }
+  const long long t0 = (long long)blockIdx.y * gridDim.x + blockIdx.x;
+  const int nm = n_miss[0];
+  if (nm <= 0 || per <= 0 || t0 >= (long long)nm * per) return;
+  const long long jstep = nblk / per, rstep = nblk % per;
+  int j = (int)(t0 / per);
+  long long r = t0 - (long long)j * per;
+  int e = miss[2 * j], sl = miss[2 * j + 1];
+  GatherTile cur = gather_tile<U>(g, e, sl, r);
+  u32x4 v[U];
+  tile_load<U, NT_LOAD>(cur, v);
+  for (;;) {
+    // advance to this workgroup's next tile
+    int jn = j + (int)jstep;
+    long long rn = r + rstep;
+    if (rn >= per) {
+      rn -= per;
+      ++jn;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = threadIdx.x + u * kGatherThreads;
-      if (i < n) {
-        if constexpr (NT_STORE)
-          __builtin_nontemporal_store(v[u], d + i);
-        else
-          d[i] = v[u];
-      }
+    if (jn >= nm) {
+      tile_store<U, NT_STORE>(cur, v);
+      break;
     }
+    if (jn != j) {
+      e = miss[2 * jn];
+      sl = miss[2 * jn + 1];
+    }
+    j = jn;
+    r = rn;
+    const GatherTile next = gather_tile<U>(g, e, sl, r);
+    u32x4 w[U];
+    tile_load<U, NT_LOAD>(next, w);
+    tile_store<U, NT_STORE>(cur, v);
+    cur = next;
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = w[u];
   }
 }
 

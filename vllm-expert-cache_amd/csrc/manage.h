@@ -99,6 +99,13 @@ __device__ __forceinline__ bool use_argmin(int nact, int S) {
   return nact * (CS + 40) <= S * CS + 256;
 }
 
+__device__ __forceinline__ long long uniform_i64(long long v) {
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned long long)v);
+  const unsigned hi =
+      (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned long long)v >> 32));
+  return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
 // One policy step. On return, the updated table is in L.tab (or in memory for GLOBAL_E)
 // and idv holds ids[lane + 64k] (or -1 past mk).
 template <int CS, bool GLOBAL_E, int IDB>
@@ -109,8 +116,10 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
 
   // ---- every independent load, issued together ---------------------------------------
   // Addresses are clamped into range instead of predicated, so no load waits behind a
-  // branch; lanes past the end substitute their sentinel after the loads return.
-  const long long st = a.step[0] + 1;
+  // branch; lanes past the end substitute their sentinel after the loads return. The step
+  // counter is a vector load: a scalar load would count in lgkmcnt, and every LDS fence
+  // below would stall on it.
+  const long long st_v = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   using IdT = typename std::conditional<IDB == 8, long long, int>::type;
   IdT raw[kIdRegs];
   if (mk > 0) {
@@ -168,75 +177,110 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       if (e < E) L.tab[e] = tv[u];
     }
     for (int base = kTabRegs * kWave; base < E; base += kTabRegs * kWave) {
+      int tw[kTabRegs];
+#pragma unroll
+      for (int u = 0; u < kTabRegs; ++u) tw[u] = a.table[min(base + lane + u * kWave, E - 1)];
 #pragma unroll
       for (int u = 0; u < kTabRegs; ++u) {
         const int e = base + lane + u * kWave;
-        tv[u] = a.table[min(e, E - 1)];
-      }
-#pragma unroll
-      for (int u = 0; u < kTabRegs; ++u) {
-        const int e = base + lane + u * kWave;
-        if (e < E) L.tab[e] = tv[u];
+        if (e < E) L.tab[e] = tw[u];
       }
     }
   }
   step_sync<GLOBAL_E>();
 
-  // ---- distinct count; the caller's `routed` is left holding the flags ----------------
-  int cnt = 0;
-  for (int base = 0; base < E; base += kWave) {
-    const int e = base + lane;
-    const bool f = e < E && flag[e];
-    if constexpr (!GLOBAL_E) {
-      if (e < E) a.routed[e] = f ? 1 : 0;
+  // ---- distinct count (the caller's `routed` is left holding the flags), then hits mark
+  // ---- their slot and misses enumerate in ascending expert id ------------------------
+  int cnt = 0, total = 0;
+  if (!GLOBAL_E && E <= kTabRegs * kWave) {
+    // the whole table is in registers: one batch of flag reads, no table re-read
+    bool fl[kTabRegs];
+#pragma unroll
+    for (int u = 0; u < kTabRegs; ++u) {
+      const int e = lane + u * kWave;
+      fl[u] = flag[min(e, E - 1)] != 0 && e < E;
     }
-    cnt += __popcll(__ballot(f));
-  }
-  if (cnt > a.max_distinct) {  // wide step: read through, nothing else changes
-    if (lane == 0) {
-      a.step[0] = st;
-      a.n_miss[0] = 0;
+#pragma unroll
+    for (int u = 0; u < kTabRegs; ++u) {
+      const int e = lane + u * kWave;
+      if (e < E) a.routed[e] = fl[u] ? 1 : 0;
+      cnt += __popcll(__ballot(fl[u]));
     }
-    return;
-  }
-
-  // ---- hits mark their slot; misses enumerate in ascending expert id -----------------
-  int total = 0;
-  for (int base = 0; base < E; base += kWave) {
-    const int e = base + lane;
-    const bool f = e < E && flag[e];
-    int t = -1;
-    if (f) {
-      if constexpr (GLOBAL_E)
-        t = a.table[e];
-      else
-        t = L.tab[e];
+    if (cnt > a.max_distinct) {  // wide step: read through, nothing else changes
+      if (lane == 0) {
+        a.step[0] = st_v + 1;
+        a.n_miss[0] = 0;
+      }
+      return;
     }
-    if (f && t >= 0 && t < S) L.hit[t] = 1;
-    const bool m = f && t < 0;
-    const unsigned long long mask = __ballot(m);
-    const int j = total + __popcll(mask & lanes_below());
-    if (m && j < a.max_inserts) {
-      L.mis[j] = e;
-      a.miss[2 * j] = e;
+#pragma unroll
+    for (int u = 0; u < kTabRegs; ++u) {
+      const int e = lane + u * kWave;
+      const int t = tv[u];
+      if (fl[u] && t >= 0 && t < S) L.hit[t] = 1;
+      const bool m = fl[u] && t < 0;
+      const unsigned long long mask = __ballot(m);
+      const int j = total + __popcll(mask & lanes_below());
+      if (m && j < a.max_inserts) {
+        L.mis[j] = e;
+        a.miss[2 * j] = e;
+      }
+      total += __popcll(mask);
     }
-    total += __popcll(mask);
+  } else {
+    for (int base = 0; base < E; base += kWave) {
+      const int e = base + lane;
+      const bool f = e < E && flag[e];
+      if constexpr (!GLOBAL_E) {
+        if (e < E) a.routed[e] = f ? 1 : 0;
+      }
+      cnt += __popcll(__ballot(f));
+    }
+    if (cnt > a.max_distinct) {
+      if (lane == 0) {
+        a.step[0] = st_v + 1;
+        a.n_miss[0] = 0;
+      }
+      return;
+    }
+    for (int base = 0; base < E; base += kWave) {
+      const int e = base + lane;
+      const bool f = e < E && flag[e];
+      int t = -1;
+      if (f) {
+        if constexpr (GLOBAL_E)
+          t = a.table[e];
+        else
+          t = L.tab[e];
+      }
+      if (f && t >= 0 && t < S) L.hit[t] = 1;
+      const bool m = f && t < 0;
+      const unsigned long long mask = __ballot(m);
+      const int j = total + __popcll(mask & lanes_below());
+      if (m && j < a.max_inserts) {
+        L.mis[j] = e;
+        a.miss[2 * j] = e;
+      }
+      total += __popcll(mask);
+    }
   }
   const int nins = min(total, a.max_inserts);
   lds_sync();
 
+  // ---- slot side: refreshed stamps, and whether each slot's expert is routed ----------
+  const long long st = uniform_i64(st_v) + 1;
   const bool lru = a.policy == 0;
+  bool fx[CS];
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
-    if (s < S && L.hit[s]) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
+    const int x = se[c];
+    const bool hit = s < S && L.hit[min(s, S - 1)];
+    fx[c] = x >= 0 && x < E && flag[min(max(x, 0), E - 1)];
+    if (hit) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
+    if (nins == 0 && hit) a.slot_stamp[s] = sp[c];
   }
   if (nins == 0) {  // no inserts: refreshed stamps only, no ageing
-#pragma unroll
-    for (int c = 0; c < CS; ++c) {
-      const int s = lane + c * kWave;
-      if (s < S && L.hit[s]) a.slot_stamp[s] = sp[c];
-    }
     if (lane == 0) {
       a.step[0] = st;
       a.n_miss[0] = 0;
@@ -257,16 +301,18 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
-    const int x = se[c];
-    ev[c] = s < S && (x < 0 || x >= E || !flag[x]);
+    ev[c] = s < S && !fx[c];
     key[c] = victim_key(sp[c], s);
     nev += __popcll(__ballot(ev[c]));
-    if (s < S) L.se[s] = x;
   }
   const int nact = min(nins, nev);
+  const long long fresh = lru ? st : 1;
 
-  // ---- victims: the nact smallest keys, ascending ------------------------------------
-  if (use_argmin<CS>(nact, S)) {
+  if (nact <= kWave && use_argmin<CS>(nact, S)) {
+    // ---- few inserts: repeated wave-min, each insert installed as soon as it is found.
+    // The victim's old expert comes from its owner lane's register, the insert r-th miss
+    // from lane r's copy of the miss list.
+    const int my_mis = L.mis[min(lane, nins - 1)];
     for (int r = 0; r < nact; ++r) {
       long long m = kKeyMax;
 #pragma unroll
@@ -274,16 +320,41 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
         if (ev[c] && key[c] < m) m = key[c];
       m = wave_min_i64(m);
       const int sl = (int)(m & kSlotMask);
+      const int csl = sl >> 6, lsl = sl & (kWave - 1);
+      const int e = __builtin_amdgcn_readlane(my_mis, r);
+      int old = -1;
 #pragma unroll
       for (int c = 0; c < CS; ++c)
-        if (lane + c * kWave == sl) ev[c] = false;
-      if (lane == 0) L.vic[r] = sl;
+        if (c == csl) old = __builtin_amdgcn_readlane(se[c], lsl);
+#pragma unroll
+      for (int c = 0; c < CS; ++c)
+        if (c == csl && lane == lsl) {
+          ev[c] = false;
+          se[c] = e;
+          sp[c] = fresh;
+        }
+      if (lane == 0) {
+        if (old >= 0 && old < E) {
+          a.table[old] = -1;
+          a.map_cold[old] = old;
+          if constexpr (!GLOBAL_E) L.tab[old] = -1;
+        }
+        a.table[e] = sl;
+        a.map_cold[e] = -1;
+        a.miss[2 * r + 1] = sl;
+        if constexpr (!GLOBAL_E) L.tab[e] = sl;
+      }
     }
   } else {
+    // ---- many inserts: rank every evictable key against all keys, then install in
+    // ---- parallel (distinct slots, distinct experts, disjoint table entries)
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
       const int s = lane + c * kWave;
-      if (s < S) L.key[s] = ev[c] ? key[c] : kKeyMax;
+      if (s < S) {
+        L.key[s] = ev[c] ? key[c] : kKeyMax;
+        L.se[s] = se[c];
+      }
     }
     if (lane == 0) L.key[S] = kKeyMax;  // pad to an even count for paired reads
     lds_sync();
@@ -299,26 +370,32 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
 #pragma unroll
     for (int c = 0; c < CS; ++c)
       if (ev[c] && rank[c] < nins) L.vic[rank[c]] = lane + c * kWave;
-  }
-  lds_sync();
-
-  // ---- installs (distinct slots, distinct experts: independent, one per lane) ---------
-  const long long fresh = lru ? st : 1;
-  for (int r = lane; r < nact; r += kWave) {
-    const int sl = L.vic[r];
-    const int e = L.mis[r];
-    const int old = L.se[sl];
-    if (old >= 0 && old < E) {
-      a.table[old] = -1;
-      a.map_cold[old] = old;
-      if constexpr (!GLOBAL_E) L.tab[old] = -1;
+    lds_sync();
+    for (int r = lane; r < nact; r += kWave) {
+      const int sl = L.vic[r];
+      const int e = L.mis[r];
+      const int old = L.se[sl];
+      if (old >= 0 && old < E) {
+        a.table[old] = -1;
+        a.map_cold[old] = old;
+        if constexpr (!GLOBAL_E) L.tab[old] = -1;
+      }
+      a.table[e] = sl;
+      a.map_cold[e] = -1;
+      a.miss[2 * r + 1] = sl;
+      if constexpr (!GLOBAL_E) L.tab[e] = sl;
+      L.fresh[sl] = 1;
+      L.se[sl] = e;
     }
-    a.table[e] = sl;
-    a.map_cold[e] = -1;
-    a.miss[2 * r + 1] = sl;
-    if constexpr (!GLOBAL_E) L.tab[e] = sl;
-    L.fresh[sl] = 1;
-    L.se[sl] = e;
+    lds_sync();
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+      const int s = lane + c * kWave;
+      if (s < S && L.fresh[s]) {
+        se[c] = L.se[s];
+        sp[c] = fresh;
+      }
+    }
   }
   step_sync<GLOBAL_E>();
 
@@ -326,10 +403,6 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
     if (s < S) {
-      if (L.fresh[s]) {
-        se[c] = L.se[s];
-        sp[c] = fresh;
-      }
       a.slot_expert[s] = se[c];
       a.slot_stamp[s] = sp[c];
     }
@@ -363,9 +436,19 @@ __device__ __forceinline__ void remap_tail(const ManageArgs& a, const ManageLds<
     store_id<IDB>(a.out, i, lookup(load_id<IDB>(a.ids, i)));
 }
 
+// Makes every kernel argument live in SGPRs at this point, so the compiler issues all the
+// argument loads together (one round trip) instead of sinking some into later branches.
+__device__ __forceinline__ void args_in_sgprs(const ManageArgs& a) {
+  asm volatile("" ::"s"(a.ids), "s"(a.table), "s"(a.map_cold), "s"(a.slot_expert),
+               "s"(a.slot_stamp), "s"(a.routed), "s"(a.step), "s"(a.miss), "s"(a.n_miss),
+               "s"(a.out), "s"(a.mk), "s"(a.E), "s"(a.S), "s"(a.max_distinct),
+               "s"(a.max_inserts), "s"(a.policy), "s"(a.decay));
+}
+
 template <int CS, bool GLOBAL_E, int IDB, bool REMAP>
 __global__ __launch_bounds__(kWave) void manage_k(ManageArgs a) {
   __shared__ ManageLds<GLOBAL_E> L;
+  args_in_sgprs(a);
   long long idv[kIdRegs];
   manage_step<CS, GLOBAL_E, IDB>(a, L, idv);
   if constexpr (REMAP) {
