@@ -194,3 +194,38 @@ def test_int64_ids_and_padding_through_fused_remap():
         assert np.array_equal(st_dev.table[0].cpu().numpy(), st_ref.table)
         assert np.array_equal(st_dev.slot_stamp[0].cpu().numpy(), st_ref.slot_stamp)
         assert np.array_equal(out.cpu().numpy(), oracle.remap(ids, st_ref.table))
+
+
+@pytest.mark.parametrize("entry", ["manage", "manage_remap", "fused"])
+def test_empty_routing(entry):
+    """mk = 0 (no routing ids, a null ids pointer): the step counter advances, nothing is
+    routed, nothing inserted; the state is otherwise untouched."""
+    E, S = 64, 16
+    st = gu.Layers(1, E, S, hot=list(range(0, 32, 2)))
+    st.slot_stamp.fill_(5)
+    before = {f: getattr(st, f).clone() for f in ("table", "map_cold", "slot_expert",
+                                                  "slot_stamp")}
+    if entry == "fused":
+        outs = {k: torch.full((n,), -5, dtype=torch.int32, device=gu.DEV) for k, n in
+                (("sorted_hot", 16), ("eids_hot", 1), ("npad_hot", 1), ("sorted_cold", 16),
+                 ("eids_cold", 1), ("npad_cold", 1))}
+        rc = gu.lib().expert_cache_fused(
+            None, 0, E, S, 0, S, st.row("table", 0), st.row("map_cold", 0),
+            st.row("slot_expert", 0), st.row("slot_stamp", 0), st.row("routed", 0),
+            st.row("step", 0), st.row("miss", 0), st.row("n_miss", 0), 16, 16, 1,
+            *[gu.ptr(outs[k]) for k in ("sorted_hot", "eids_hot", "npad_hot", "sorted_cold",
+                                        "eids_cold", "npad_cold")], gu.stream())
+    elif entry == "manage":
+        rc = gu.manage_call(gu.lib(), st, 0, None, 0, 0, S, LFU, 64)
+    else:
+        out = torch.full((1,), -5, dtype=torch.int32, device=gu.DEV)
+        rc = gu.manage_call(gu.lib(), st, 0, None, 0, 0, S, LFU, 64, out_ptr=gu.ptr(out))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(st.step[0, 0]) == 1 and int(st.n_miss[0, 0]) == 0
+    assert int(st.routed.sum()) == 0
+    for f, t in before.items():
+        assert torch.equal(getattr(st, f), t), f
+    if entry == "fused":
+        assert outs["npad_hot"].item() == 0 and outs["npad_cold"].item() == 0
+        assert (outs["sorted_hot"] == 0).all() and (outs["eids_hot"] == -1).all()

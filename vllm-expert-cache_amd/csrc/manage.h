@@ -59,7 +59,7 @@ struct ManageLds {
   unsigned char fresh[kMaxSlots];  // slot received an insert this step
   int tab[GLOBAL_E ? 1 : kLdsExperts];
   int se[kMaxSlots];               // slot -> expert, for the installs
-  long long key[kMaxSlots + 2];    // rank path: key or INT64_MAX
+  alignas(16) long long key[kMaxSlots + 8];  // rank path: key or INT64_MAX, padded to 8
   int vic[kMaxInserts];            // insert r -> victim slot
   int mis[kMaxInserts];            // insert r -> missing expert
 };
@@ -92,11 +92,12 @@ __device__ __forceinline__ long long victim_key(long long stamp, int slot) {
   return (long long)(((unsigned long long)stamp << kSlotBits) | (unsigned long long)slot);
 }
 
-// Which victim search is cheaper: nact wave-min reductions (~CS + 40 instructions each)
-// or one rank pass (S keys from LDS against CS keys per lane).
+// Which victim search is cheaper, in cycles measured on gfx950: a wave-min reduction plus
+// its install per insert (~500 + 12 per key held by a lane), or one pass ranking every
+// evictable key against all nev of them (~12 per key per lane, ~800 fixed).
 template <int CS>
-__device__ __forceinline__ bool use_argmin(int nact, int S) {
-  return nact * (CS + 40) <= S * CS + 256;
+__device__ __forceinline__ bool use_argmin(int nact, int nev) {
+  return nact <= kWave && nact * (500 + 12 * CS) <= nev * 12 * CS + 800;
 }
 
 __device__ __forceinline__ long long uniform_i64(long long v) {
@@ -120,13 +121,15 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   // counter is a vector load: a scalar load would count in lgkmcnt, and every LDS fence
   // below would stall on it.
   const long long st_v = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // No branch around the id loads either (a branch join would make the compiler wait for
+  // them before issuing the rest): with no ids, they read the 8-byte step counter instead.
   using IdT = typename std::conditional<IDB == 8, long long, int>::type;
+  const IdT* ip = mk > 0 ? reinterpret_cast<const IdT*>(a.ids)
+                         : reinterpret_cast<const IdT*>(a.step);
+  const int last_id = mk > 0 ? mk - 1 : 0;
   IdT raw[kIdRegs];
-  if (mk > 0) {
 #pragma unroll
-    for (int k = 0; k < kIdRegs; ++k)
-      raw[k] = reinterpret_cast<const IdT*>(a.ids)[min(lane + k * kWave, mk - 1)];
-  }
+  for (int k = 0; k < kIdRegs; ++k) raw[k] = ip[min(lane + k * kWave, last_id)];
   int se[CS];
   long long sp[CS];
 #pragma unroll
@@ -140,13 +143,6 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
 #pragma unroll
     for (int u = 0; u < kTabRegs; ++u) tv[u] = a.table[min(lane + u * kWave, E - 1)];
   }
-#pragma unroll
-  for (int k = 0; k < kIdRegs; ++k)
-    idv[k] = (mk > 0 && lane + k * kWave < mk) ? (long long)raw[k] : -1;
-#pragma unroll
-  for (int c = 0; c < CS; ++c)
-    if (lane + c * kWave >= S) se[c] = -1;
-
   unsigned char* flag;
   if constexpr (GLOBAL_E)
     flag = a.routed;
@@ -161,6 +157,14 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   step_sync<GLOBAL_E>();
 
   // ---- routed flags (ids outside [0,E) are padding; int64 ids truncate like .to(int32))
+  // The sentinels for lanes past mk / S are applied only now, after the first fence, so
+  // that fence does not wait for the loads.
+#pragma unroll
+  for (int k = 0; k < kIdRegs; ++k)
+    idv[k] = (mk > 0 && lane + k * kWave < mk) ? (long long)raw[k] : -1;
+#pragma unroll
+  for (int c = 0; c < CS; ++c)
+    if (lane + c * kWave >= S) se[c] = -1;
 #pragma unroll
   for (int k = 0; k < kIdRegs; ++k) {
     const int e = (int)idv[k];
@@ -193,7 +197,9 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   // ---- their slot and misses enumerate in ascending expert id ------------------------
   int cnt = 0, total = 0;
   if (!GLOBAL_E && E <= kTabRegs * kWave) {
-    // the whole table is in registers: one batch of flag reads, no table re-read
+    // the whole table is in registers: one batch of flag reads, no table re-read; chunks
+    // past E are skipped on a uniform branch
+    const int nchunk = (E + kWave - 1) / kWave;
     bool fl[kTabRegs];
 #pragma unroll
     for (int u = 0; u < kTabRegs; ++u) {
@@ -202,9 +208,11 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     }
 #pragma unroll
     for (int u = 0; u < kTabRegs; ++u) {
-      const int e = lane + u * kWave;
-      if (e < E) a.routed[e] = fl[u] ? 1 : 0;
-      cnt += __popcll(__ballot(fl[u]));
+      if (u < nchunk) {
+        const int e = lane + u * kWave;
+        if (e < E) a.routed[e] = fl[u] ? 1 : 0;
+        cnt += __popcll(__ballot(fl[u]));
+      }
     }
     if (cnt > a.max_distinct) {  // wide step: read through, nothing else changes
       if (lane == 0) {
@@ -215,17 +223,19 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     }
 #pragma unroll
     for (int u = 0; u < kTabRegs; ++u) {
-      const int e = lane + u * kWave;
-      const int t = tv[u];
-      if (fl[u] && t >= 0 && t < S) L.hit[t] = 1;
-      const bool m = fl[u] && t < 0;
-      const unsigned long long mask = __ballot(m);
-      const int j = total + __popcll(mask & lanes_below());
-      if (m && j < a.max_inserts) {
-        L.mis[j] = e;
-        a.miss[2 * j] = e;
+      if (u < nchunk) {
+        const int e = lane + u * kWave;
+        const int t = tv[u];
+        if (fl[u] && t >= 0 && t < S) L.hit[t] = 1;
+        const bool m = fl[u] && t < 0;
+        const unsigned long long mask = __ballot(m);
+        const int j = total + __popcll(mask & lanes_below());
+        if (m && j < a.max_inserts) {
+          L.mis[j] = e;
+          a.miss[2 * j] = e;
+        }
+        total += __popcll(mask);
       }
-      total += __popcll(mask);
     }
   } else {
     for (int base = 0; base < E; base += kWave) {
@@ -308,7 +318,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   const int nact = min(nins, nev);
   const long long fresh = lru ? st : 1;
 
-  if (nact <= kWave && use_argmin<CS>(nact, S)) {
+  if (use_argmin<CS>(nact, nev)) {
     // ---- few inserts: repeated wave-min, each insert installed as soon as it is found.
     // The victim's old expert comes from its owner lane's register, the insert r-th miss
     // from lane r's copy of the miss list.
@@ -346,26 +356,34 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       }
     }
   } else {
-    // ---- many inserts: rank every evictable key against all keys, then install in
-    // ---- parallel (distinct slots, distinct experts, disjoint table entries)
+    // ---- many inserts: the evictable keys are compacted into L.key, each is ranked
+    // ---- against all of them, then the installs run in parallel (distinct slots,
+    // ---- distinct experts, disjoint table entries)
+    int base = 0;
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
       const int s = lane + c * kWave;
-      if (s < S) {
-        L.key[s] = ev[c] ? key[c] : kKeyMax;
-        L.se[s] = se[c];
-      }
+      const unsigned long long mask = __ballot(ev[c]);
+      if (ev[c]) L.key[base + __popcll(mask & lanes_below())] = key[c];
+      if (s < S) L.se[s] = se[c];
+      base += __popcll(mask);
     }
-    if (lane == 0) L.key[S] = kKeyMax;  // pad to an even count for paired reads
+    const int n8 = (nev + 7) & ~7;
+    if (lane < n8 - nev) L.key[nev + lane] = kKeyMax;  // pad to a multiple of 8
     lds_sync();
     int rank[CS];
 #pragma unroll
     for (int c = 0; c < CS; ++c) rank[c] = 0;
-    const int S2 = (S + 1) & ~1;
-    for (int j = 0; j < S2; j += 2) {
-      const long long k0 = L.key[j], k1 = L.key[j + 1];
+    // every lane reads the same keys (an LDS broadcast), 8 per batch so the reads of a
+    // batch are in flight together
+    typedef long long i64x2 __attribute__((ext_vector_type(2)));
+    const i64x2* kp = reinterpret_cast<const i64x2*>(L.key);
+    for (int j = 0; j < n8; j += 8) {
+      const i64x2 k01 = kp[j / 2], k23 = kp[j / 2 + 1], k45 = kp[j / 2 + 2], k67 = kp[j / 2 + 3];
 #pragma unroll
-      for (int c = 0; c < CS; ++c) rank[c] += (k0 < key[c]) + (k1 < key[c]);
+      for (int c = 0; c < CS; ++c)
+        rank[c] += (k01.x < key[c]) + (k01.y < key[c]) + (k23.x < key[c]) + (k23.y < key[c]) +
+                   (k45.x < key[c]) + (k45.y < key[c]) + (k67.x < key[c]) + (k67.y < key[c]);
     }
 #pragma unroll
     for (int c = 0; c < CS; ++c)
