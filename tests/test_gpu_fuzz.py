@@ -1,0 +1,82 @@
+"""Randomised policy-step parity: arbitrary shapes and arguments against the oracle.
+
+Every case draws E (including above the 4096 experts held in LDS), S (including S > E and
+S up to 1024), mk (including 0 and more than 256 ids), ids with padding and out-of-range
+values, max_distinct (including below the routed count: read-through), max_inserts
+(including 0 and caps below the miss count), policy and decay, and a random consistent warm
+state with random stamps. Each step is compared on every field, and the fused remap output
+against the closed form.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import gpu_util as gu
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+CASES = 120
+STEPS = 12
+
+
+def _case(seed: int):
+    rng = np.random.default_rng(seed)
+    E = int(rng.choice([1, 2, 7, 64, 128, 200, 257, 512, 1000, 4096, 4100, 6000]))
+    S = int(rng.choice([1, 2, 3, 16, 63, 64, 65, 128, 129, 300, 513, 1024]))
+    mk = int(rng.choice([0, 1, 8, 33, 64, 200, 257, 300, 700]))
+    mi = int(rng.choice([0, 1, 4, S, min(S + 5, 1024), 1024]))
+    policy = int(rng.integers(0, 2))
+    decay = int(rng.choice([0, 1, 3, 64]))
+    nhot = int(rng.integers(0, min(S, E) + 1))
+    hot = rng.choice(E, nhot, replace=False)
+    slots = rng.choice(S, nhot, replace=False)
+    stamps = rng.integers(0, 1000, size=S)
+    return rng, E, S, mk, mi, policy, decay, hot, slots, stamps
+
+
+def _device_state(E, S, mi, hot, slots, stamps):
+    st = gu.Layers(1, E, S, miss_cap=max(mi, 1))
+    table = np.full(E, -1, np.int32)
+    cold = np.arange(E, dtype=np.int32)
+    se = np.full(S, -1, np.int32)
+    table[hot] = slots
+    cold[hot] = -1
+    se[slots] = hot
+    st.table[0] = torch.as_tensor(table)
+    st.map_cold[0] = torch.as_tensor(cold)
+    st.slot_expert[0] = torch.as_tensor(se)
+    st.slot_stamp[0] = torch.as_tensor(stamps)
+    ref = oracle.State(E, S, miss_cap=max(mi, 1))
+    ref.table[:], ref.map_cold[:], ref.slot_expert[:] = table, cold, se
+    ref.slot_stamp[:] = stamps
+    return st, ref
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_shapes(seed):
+    rng, E, S, mk, mi, policy, decay, hot, slots, stamps = _case(seed)
+    st, ref = _device_state(E, S, mi, hot, slots, stamps)
+    fused_remap = seed % 2 == 0
+    for t in range(STEPS):
+        ids = rng.integers(-3, E + 3, size=mk).astype(np.int32)
+        distinct = len(np.unique(ids[(ids >= 0) & (ids < E)]))
+        md = int(rng.choice([distinct, distinct - 1, E, mk, -1]))
+        d_ids = torch.as_tensor(ids, device=gu.DEV)
+        out = torch.full((max(mk, 1),), -9, dtype=torch.int32, device=gu.DEV)
+        rc = gu.manage_call(gu.lib(), st, 0, gu.ptr(d_ids) if mk else None, mk, md, mi,
+                            policy, decay, gu.ptr(out) if fused_remap else None)
+        assert rc == 0
+        assert ref.manage(ids, md, mi, policy, decay) == 0
+        torch.cuda.synchronize()
+        tag = f"seed {seed} step {t}: E={E} S={S} mk={mk} md={md} mi={mi} pol={policy} dec={decay}"
+        for name, dev in (("table", st.table[0]), ("map_cold", st.map_cold[0]),
+                          ("slot_expert", st.slot_expert[0]), ("slot_stamp", st.slot_stamp[0]),
+                          ("routed", st.routed[0]), ("step", st.step[0]), ("miss", st.miss[0]),
+                          ("n_miss", st.n_miss[0])):
+            got, want = dev.cpu().numpy(), getattr(ref, name)
+            assert np.array_equal(got, want), f"{tag}: {name} differs at {gu.first_diff(got, want)}"
+        if fused_remap and mk:
+            assert np.array_equal(out.cpu().numpy()[:mk], oracle.remap(ids, ref.table)), tag

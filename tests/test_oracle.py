@@ -309,3 +309,30 @@ def test_fused_matches_brute_force_align(bs):
         want = _align_brute(row.tolist(), st.table, E, S, bs, L, NB)
         for k, v in want.items():
             assert np.array_equal(got[k], v), (t, k)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_serial_equals_rank_on_random_shapes(seed):
+    """The GPU fuzz's shape and argument space (tests/test_gpu_fuzz.py), both oracle forms."""
+    rng = np.random.default_rng(1000 + seed)
+    E = int(rng.choice([1, 2, 7, 64, 128, 257, 1000, 4100]))
+    S = int(rng.choice([1, 2, 3, 16, 64, 65, 129, 300, 1024]))
+    mk = int(rng.choice([0, 1, 8, 33, 257, 700]))
+    mi = int(rng.choice([0, 1, 4, S, 1024]))
+    policy, decay = int(rng.integers(0, 2)), int(rng.choice([0, 1, 3, 64]))
+    nhot = int(rng.integers(0, min(S, E) + 1))
+    hot, slots = rng.choice(E, nhot, replace=False), rng.choice(S, nhot, replace=False)
+    a, b = State(E, S, miss_cap=max(mi, 1)), State(E, S, miss_cap=max(mi, 1))
+    for st in (a, b):
+        st.table[hot] = slots
+        st.map_cold[hot] = -1
+        st.slot_expert[slots] = hot
+        st.slot_stamp[:] = rng.integers(0, 1000, size=S) if st is a else a.slot_stamp
+    for t in range(10):
+        ids = rng.integers(-3, E + 3, size=mk).astype(np.int32)
+        md = int(rng.choice([E, mk, -1, len(np.unique(ids[(ids >= 0) & (ids < E)])) - 1]))
+        assert a.manage(ids, md, mi, policy, decay, "serial") == 0
+        assert b.manage(ids, md, mi, policy, decay, "rank") == 0
+        for f in State.FIELDS:
+            assert np.array_equal(getattr(a, f), getattr(b, f)), (seed, t, f)
+        _check_invariants(b)
