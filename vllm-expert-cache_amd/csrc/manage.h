@@ -14,9 +14,10 @@
 //  * Victims are the nact smallest keys (stamp << 20 | slot) among the slots whose expert
 //    is not routed this step, assigned in ascending key order to the misses in ascending
 //    id order. Few inserts: repeated DPP wave-min (one 6-step DPP reduction per insert).
-//    Many inserts: every evictable key is ranked against all keys broadcast from LDS.
-//    Both give the same assignment (keys are unique, installing does not change any other
-//    slot's key or evictability).
+//    Many inserts: a binary search on the key value finds the nact-th smallest key (each
+//    probe one ballot count per register chunk); the victims at or below it are ranked
+//    among themselves. Both give the same assignment (keys are unique, installing does not
+//    change any other slot's key or evictability).
 //  * A fused tail rewrites the caller's routing ids into slot ids against the updated table
 //    (vllm_expert_cache/cache.py:108-110 semantics, negative ids wrapping).
 #pragma once
@@ -54,12 +55,11 @@ struct ManageArgs {
 // read the table from memory; the LDS arrays for them shrink to one element.
 template <bool GLOBAL_E>
 struct ManageLds {
-  unsigned char flag[GLOBAL_E ? 1 : kLdsExperts];
-  unsigned char hit[kMaxSlots];    // slot refreshed by a routed expert this step
-  unsigned char fresh[kMaxSlots];  // slot received an insert this step
+  alignas(16) unsigned char flag[GLOBAL_E ? 16 : kLdsExperts];  // cleared 16 bytes a lane
+  alignas(16) unsigned char hit[kMaxSlots];  // slot refreshed by a routed expert this step
   int tab[GLOBAL_E ? 1 : kLdsExperts];
   int se[kMaxSlots];               // slot -> expert, for the installs
-  alignas(16) long long key[kMaxSlots + 8];  // rank path: key or INT64_MAX, padded to 8
+  alignas(16) long long key[kMaxSlots + 8];  // select path: victim keys, INT64_MAX padded
   int vic[kMaxInserts];            // insert r -> victim slot
   int mis[kMaxInserts];            // insert r -> missing expert
 };
@@ -92,12 +92,13 @@ __device__ __forceinline__ long long victim_key(long long stamp, int slot) {
   return (long long)(((unsigned long long)stamp << kSlotBits) | (unsigned long long)slot);
 }
 
-// Which victim search is cheaper, in cycles measured on gfx950: a wave-min reduction plus
-// its install per insert (~500 + 12 per key held by a lane), or one pass ranking every
-// evictable key against all nev of them (~12 per key per lane, ~800 fixed).
+// Which victim search is cheaper: a wave-min reduction plus its install per insert, or
+// the threshold select (a fixed cost of about two wave-min reductions, ~20 ballot-count
+// probes and one parallel install pass).
 template <int CS>
 __device__ __forceinline__ bool use_argmin(int nact, int nev) {
-  return nact <= kWave && nact * (500 + 12 * CS) <= nev * 12 * CS + 800;
+  (void)nev;
+  return nact <= (CS <= 2 ? 2 : 3);
 }
 
 __device__ __forceinline__ long long uniform_i64(long long v) {
@@ -149,11 +150,16 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   else
     flag = L.flag;
 
-  for (int e = lane; e < E; e += kWave) flag[e] = 0;
-  for (int s = lane; s < S; s += kWave) {
-    L.hit[s] = 0;
-    L.fresh[s] = 0;
+  // clears: 16 bytes per lane per store (E <= 4096 and S <= 1024 stay inside the arrays)
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  if constexpr (GLOBAL_E) {
+    for (int e = lane; e < E; e += kWave) flag[e] = 0;
+  } else {
+    for (int i = lane * 16; i < E; i += kWave * 16)
+      *reinterpret_cast<u32x4*>(&L.flag[i]) = u32x4{0, 0, 0, 0};
   }
+  for (int i = lane * 16; i < S; i += kWave * 16)
+    *reinterpret_cast<u32x4*>(&L.hit[i]) = u32x4{0, 0, 0, 0};
   step_sync<GLOBAL_E>();
 
   // ---- routed flags (ids outside [0,E) are padding; int64 ids truncate like .to(int32))
@@ -175,11 +181,9 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     if (e >= 0 && e < E) flag[e] = 1;
   }
   if constexpr (!GLOBAL_E) {
+    // entries past E (below 512) are written too: nothing reads them
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) {
-      const int e = lane + u * kWave;
-      if (e < E) L.tab[e] = tv[u];
-    }
+    for (int u = 0; u < kTabRegs; ++u) L.tab[lane + u * kWave] = tv[u];
     for (int base = kTabRegs * kWave; base < E; base += kTabRegs * kWave) {
       int tw[kTabRegs];
 #pragma unroll
@@ -200,17 +204,17 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     // the whole table is in registers: one batch of flag reads, no table re-read; chunks
     // past E are skipped on a uniform branch
     const int nchunk = (E + kWave - 1) / kWave;
+    unsigned char fb[kTabRegs];
     bool fl[kTabRegs];
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) {
-      const int e = lane + u * kWave;
-      fl[u] = flag[min(e, E - 1)] != 0 && e < E;
-    }
+    for (int u = 0; u < kTabRegs; ++u) fb[u] = flag[min(lane + u * kWave, E - 1)];
+#pragma unroll
+    for (int u = 0; u < kTabRegs; ++u) fl[u] = (fb[u] != 0) & (lane + u * kWave < E);
 #pragma unroll
     for (int u = 0; u < kTabRegs; ++u) {
       if (u < nchunk) {
-        const int e = lane + u * kWave;
-        if (e < E) a.routed[e] = fl[u] ? 1 : 0;
+        // lanes past E store routed[E-1]'s own flag there: no store needs a branch
+        a.routed[min(lane + u * kWave, E - 1)] = fb[u] != 0 ? 1 : 0;
         cnt += __popcll(__ballot(fl[u]));
       }
     }
@@ -230,10 +234,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
         const bool m = fl[u] && t < 0;
         const unsigned long long mask = __ballot(m);
         const int j = total + __popcll(mask & lanes_below());
-        if (m && j < a.max_inserts) {
-          L.mis[j] = e;
-          a.miss[2 * j] = e;
-        }
+        if (m && j < a.max_inserts) L.mis[j] = e;
         total += __popcll(mask);
       }
     }
@@ -267,10 +268,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       const bool m = f && t < 0;
       const unsigned long long mask = __ballot(m);
       const int j = total + __popcll(mask & lanes_below());
-      if (m && j < a.max_inserts) {
-        L.mis[j] = e;
-        a.miss[2 * j] = e;
-      }
+      if (m && j < a.max_inserts) L.mis[j] = e;
       total += __popcll(mask);
     }
   }
@@ -281,12 +279,20 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   const long long st = uniform_i64(st_v) + 1;
   const bool lru = a.policy == 0;
   bool fx[CS];
+  // all flag reads first, with clamped indexes, so they are in flight together (a
+  // short-circuit test would put each read behind its own branch and wait)
+  unsigned char hv[CS], fv[CS];
+#pragma unroll
+  for (int c = 0; c < CS; ++c) {
+    hv[c] = L.hit[min(lane + c * kWave, S - 1)];
+    fv[c] = flag[min(max(se[c], 0), E - 1)];
+  }
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
     const int x = se[c];
-    const bool hit = s < S && L.hit[min(s, S - 1)];
-    fx[c] = x >= 0 && x < E && flag[min(max(x, 0), E - 1)];
+    const bool hit = (s < S) & (hv[c] != 0);
+    fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
     if (hit) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
     if (nins == 0 && hit) a.slot_stamp[s] = sp[c];
   }
@@ -356,67 +362,134 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       }
     }
   } else {
-    // ---- many inserts: the evictable keys are compacted into L.key, each is ranked
-    // ---- against all of them, then the installs run in parallel (distinct slots,
-    // ---- distinct experts, disjoint table entries)
-    int base = 0;
+    // ---- many inserts: threshold select. With h = key >> 20 (the stamp bits), sigma is
+    // ---- the smallest h such that at least nact evictable keys have h <= sigma, found by
+    // ---- binary search with one ballot count per register chunk per probe. Every
+    // ---- evictable key below bucket sigma is a victim; the rest of the nact come from
+    // ---- bucket sigma in slot order (= key order within a bucket). Each lane then installs
+    // ---- its own victims from registers (distinct slots, distinct experts, disjoint table
+    // ---- entries, so the installs need no ordering among themselves).
+    long long kmin = kKeyMax, nmax = kKeyMax;  // smallest key, and ~largest key
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
-      const int s = lane + c * kWave;
-      const unsigned long long mask = __ballot(ev[c]);
-      if (ev[c]) L.key[base + __popcll(mask & lanes_below())] = key[c];
-      if (s < S) L.se[s] = se[c];
-      base += __popcll(mask);
+      if (ev[c] && key[c] < kmin) kmin = key[c];
+      if (ev[c] && ~key[c] < nmax) nmax = ~key[c];
     }
-    const int n8 = (nev + 7) & ~7;
-    if (lane < n8 - nev) L.key[nev + lane] = kKeyMax;  // pad to a multiple of 8
-    lds_sync();
-    int rank[CS];
-#pragma unroll
-    for (int c = 0; c < CS; ++c) rank[c] = 0;
-    // every lane reads the same keys (an LDS broadcast), 8 per batch so the reads of a
-    // batch are in flight together
-    typedef long long i64x2 __attribute__((ext_vector_type(2)));
-    const i64x2* kp = reinterpret_cast<const i64x2*>(L.key);
-    for (int j = 0; j < n8; j += 8) {
-      const i64x2 k01 = kp[j / 2], k23 = kp[j / 2 + 1], k45 = kp[j / 2 + 2], k67 = kp[j / 2 + 3];
+    const long long hmin = wave_min_i64(kmin) >> kSlotBits;
+    const long long hmax = (~wave_min_i64(nmax)) >> kSlotBits;
+    long long sigma;
+    if ((unsigned long long)(hmax - hmin) < (1ull << 31)) {
+      // stamp spreads below 2^31: 32-bit compares on h - hmin (non-evictable: all ones)
+      unsigned rel[CS];
 #pragma unroll
       for (int c = 0; c < CS; ++c)
-        rank[c] += (k01.x < key[c]) + (k01.y < key[c]) + (k23.x < key[c]) + (k23.y < key[c]) +
-                   (k45.x < key[c]) + (k45.y < key[c]) + (k67.x < key[c]) + (k67.y < key[c]);
-    }
+        rel[c] = ev[c] ? (unsigned)((key[c] >> kSlotBits) - hmin) : 0xFFFFFFFFu;
+      unsigned lo = 0, hi = (unsigned)(hmax - hmin);
+      while (lo < hi) {
+        const unsigned mid = (lo + hi) >> 1;
+        int n = 0;
 #pragma unroll
-    for (int c = 0; c < CS; ++c)
-      if (ev[c] && rank[c] < nins) L.vic[rank[c]] = lane + c * kWave;
-    lds_sync();
-    for (int r = lane; r < nact; r += kWave) {
-      const int sl = L.vic[r];
-      const int e = L.mis[r];
-      const int old = L.se[sl];
-      if (old >= 0 && old < E) {
-        a.table[old] = -1;
-        a.map_cold[old] = old;
-        if constexpr (!GLOBAL_E) L.tab[old] = -1;
+        for (int c = 0; c < CS; ++c) n += __popcll(__ballot(rel[c] <= mid));
+        if (n >= nact)
+          hi = mid;
+        else
+          lo = mid + 1;
       }
-      a.table[e] = sl;
-      a.map_cold[e] = -1;
-      a.miss[2 * r + 1] = sl;
-      if constexpr (!GLOBAL_E) L.tab[e] = sl;
-      L.fresh[sl] = 1;
-      L.se[sl] = e;
+      sigma = hmin + (long long)lo;
+    } else {
+      long long lo = hmin, hi = hmax;
+      while (lo < hi) {
+        const long long mid = lo + ((hi - lo) >> 1);
+        int n = 0;
+#pragma unroll
+        for (int c = 0; c < CS; ++c) n += __popcll(__ballot(ev[c] && (key[c] >> kSlotBits) <= mid));
+        if (n >= nact)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      sigma = lo;
     }
-    lds_sync();
+
+    // victims: below bucket sigma, or in it among the first `need` by slot
+    bool below[CS], inb[CS];
+    int nbelow = 0;
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
-      const int s = lane + c * kWave;
-      if (s < S && L.fresh[s]) {
-        se[c] = L.se[s];
+      const long long h = key[c] >> kSlotBits;
+      below[c] = ev[c] && h < sigma;
+      inb[c] = ev[c] && h == sigma;
+      nbelow += __popcll(__ballot(below[c]));
+    }
+    const int need = nact - nbelow;
+    int pos[CS];  // insert index of each victim, or -1
+    int seen_b = 0, seen_in = 0;
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+      const unsigned long long mb = __ballot(below[c]), mi = __ballot(inb[c]);
+      const int rb = seen_b + __popcll(mb & lanes_below());
+      const int ri = seen_in + __popcll(mi & lanes_below());
+      pos[c] = inb[c] && ri < need ? nbelow + ri : -1;
+      if (below[c]) {
+        L.key[rb] = key[c];
+        pos[c] = rb;  // compaction index until ranked
+      }
+      seen_b += __popcll(mb);
+      seen_in += __popcll(mi);
+    }
+    if (nbelow > 0) {
+      // victims below the bucket take inserts 0..nbelow-1 in key order: rank each among
+      // them (every lane reads the same keys, an LDS broadcast, 8 per batch)
+      const int n8 = (nbelow + 7) & ~7;
+      if (lane < n8 - nbelow) L.key[nbelow + lane] = kKeyMax;
+      lds_sync();
+      typedef long long i64x2 __attribute__((ext_vector_type(2)));
+      const i64x2* kp = reinterpret_cast<const i64x2*>(L.key);
+      for (int j0 = 0; j0 < nbelow; j0 += kWave) {
+        const int j = j0 + lane;
+        const long long kj = L.key[min(j, n8 - 1)];
+        int rank = 0;
+        for (int i = 0; i < n8; i += 8) {
+          const i64x2 k01 = kp[i / 2], k23 = kp[i / 2 + 1], k45 = kp[i / 2 + 2],
+                      k67 = kp[i / 2 + 3];
+          rank += (k01.x < kj) + (k01.y < kj) + (k23.x < kj) + (k23.y < kj) + (k45.x < kj) +
+                  (k45.y < kj) + (k67.x < kj) + (k67.y < kj);
+        }
+        if (j < nbelow) L.vic[j] = rank;
+      }
+      lds_sync();
+#pragma unroll
+      for (int c = 0; c < CS; ++c)
+        if (below[c]) pos[c] = L.vic[pos[c]];
+    }
+
+    // installs, each by the lane holding the victim slot
+    int ne[CS];
+#pragma unroll
+    for (int c = 0; c < CS; ++c) ne[c] = L.mis[max(pos[c], 0)];
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+      if (pos[c] >= 0) {
+        const int s = lane + c * kWave;
+        const int old = se[c], e = ne[c];
+        if (old >= 0 && old < E) {
+          a.table[old] = -1;
+          a.map_cold[old] = old;
+          if constexpr (!GLOBAL_E) L.tab[old] = -1;
+        }
+        a.table[e] = s;
+        a.map_cold[e] = -1;
+        a.miss[2 * pos[c] + 1] = s;
+        if constexpr (!GLOBAL_E) L.tab[e] = s;
+        se[c] = e;
         sp[c] = fresh;
       }
     }
   }
   step_sync<GLOBAL_E>();
 
+  // the caller's miss list gets every counted miss id (miss[2j], j < nins), also past nact
+  for (int j = lane; j < nins; j += kWave) a.miss[2 * j] = L.mis[j];
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
