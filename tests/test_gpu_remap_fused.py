@@ -90,12 +90,14 @@ def test_fused_matches_oracle_and_reference(name, S, bs):
         assert np.array_equal(mine.miss[0].cpu().numpy(), ref.miss)
 
 
-def test_fused_wide_step_is_token_ordered():
+@pytest.mark.parametrize("mk", [1000, 13000])
+def test_fused_wide_step_is_token_ordered(mk):
     """mk > 256 (a prefill-sized chunk): bucket contents in token order, and the same
-    buckets as the reference's (which orders them by LDS atomics there)."""
+    buckets as the reference's (which orders them by LDS atomics there). 13000 ids make
+    outputs too large to build in LDS, so they take the path that fills memory first."""
     E, S, bs = 64, 32, 16
     rng = np.random.default_rng(4)
-    ids = rng.integers(-2, E, size=1000).astype(np.int32)
+    ids = rng.integers(-2, E, size=mk).astype(np.int32)
     L, NB = align_lengths(ids.size, E, bs)
     st, ref = gu.Layers(1, E, S), oracle.State(E, S)
     outs = _outs(L, NB)
@@ -122,3 +124,28 @@ def test_fused_wide_step_is_token_ordered():
             blocks = np.nonzero(e == bucket)[0]
             sl = slice(blocks[0] * bs, (blocks[-1] + 1) * bs)
             assert sorted(a[sl].tolist()) == sorted(b[sl].tolist()), (side, bucket)
+
+
+@pytest.mark.parametrize("bs", [1, 3, 16])
+def test_fused_outputs_at_any_alignment(bs):
+    """Output buffers 4 bytes past a 16-byte boundary take the scalar fill path; the bytes
+    must be the same as with aligned buffers, and nothing outside the buffers changes."""
+    w = traces.WORKLOADS["8-layer-e256-fp8"]
+    ids = traces.routing(w, 1, 12)
+    E, S, mk = w.experts, 128, ids.shape[1]
+    L, NB = align_lengths(mk, E, bs)
+    ref = oracle.State(E, S)
+    st = gu.Layers(1, E, S)
+    d_ids = torch.as_tensor(ids, device=gu.DEV)
+    for t in range(ids.shape[0]):
+        backing = {k: torch.full((n + 2,), -7, dtype=torch.int32, device=gu.DEV) for k, n in
+                   (("sorted_hot", L), ("eids_hot", NB), ("npad_hot", 1),
+                    ("sorted_cold", L), ("eids_cold", NB), ("npad_cold", 1))}
+        outs = {k: v[1:-1] for k, v in backing.items()}
+        assert _fused_call(gu.lib(), st, d_ids[t], mk, bs, L, NB, outs) == 0
+        rc, want = ref.fused(ids[t], min(E, mk), S, bs, L, NB)
+        assert rc == 0
+        torch.cuda.synchronize()
+        for k, v in want.items():
+            assert np.array_equal(outs[k].cpu().numpy(), v), (t, k)
+            assert backing[k][0].item() == -7 and backing[k][-1].item() == -7, (t, k)

@@ -7,6 +7,10 @@
 // multiple of the block size, scans, and places each id at its bucket offset plus its rank
 // among the earlier ids of the same bucket, so the output is in token order within every
 // bucket for every mk (the reference is token-ordered for mk <= 256 and unordered above).
+// Below each side's padded total the outputs are built in LDS (padding, block expert ids,
+// then the placed ids) and copied out with coalesced stores; past it the defaults go
+// straight to memory. No output position is written twice, so no fence is needed; outputs
+// too large for LDS are filled with their defaults in memory first and fenced.
 #pragma once
 #include "manage.h"
 
@@ -24,11 +28,17 @@ struct AlignArgs {
   int* npad_cold;
 };
 
+// Per side, the ids and block expert ids below the padded total are built in LDS and
+// copied out once when they fit in kStage ints (decode and chunked-prefill shapes).
+constexpr int kStage = 10240;
+
 struct AlignLds {
   int cur_h[kMaxSlots + 1];          // counts, then placement cursors, per slot bucket
   int cur_c[kMaxAlignExperts + 1];   // same per expert bucket
   int cum_h[kMaxSlots + 1];
   int cum_c[kMaxAlignExperts + 1];
+  unsigned long long lanes[kMaxSlots + kMaxAlignExperts];  // per bucket key: lanes of a block
+  alignas(16) int stage[2][kStage];  // per side: sorted, then expert ids from round4(n)
 };
 
 // Combined bucket key of one routing id: slot s (hot), kMaxSlots + e (cold), -1 (skipped).
@@ -38,45 +48,113 @@ __device__ __forceinline__ int align_key(int e, int E, int S, const int* tab) {
   return ((unsigned)s < (unsigned)S) ? s : kMaxSlots + e;
 }
 
+// x / bs for the wave-uniform block size: a shift for powers of two (vLLM's block sizes).
+struct BlockDiv {
+  int bs, shift;
+  __device__ __forceinline__ explicit BlockDiv(int b)
+      : bs(b), shift((b & (b - 1)) == 0 ? __builtin_ctz((unsigned)b) : -1) {}
+  __device__ __forceinline__ int div(int x) const { return shift >= 0 ? x >> shift : x / bs; }
+  __device__ __forceinline__ int pad(int x) const { return div(x + bs - 1) * bs; }
+};
+
 // Exclusive scan of block-padded counts over nb buckets; each lane owns a contiguous run.
-__device__ __forceinline__ void padded_scan(const int* cnt, int* cum, int nb, int bs) {
+__device__ __forceinline__ void padded_scan(const int* cnt, int* cum, int nb, BlockDiv d) {
   const int lane = __lane_id();
   const int per = (nb + kWave - 1) / kWave;
   const int lo = min(lane * per, nb), hi = min(lo + per, nb);
   int local = 0;
-  for (int b = lo; b < hi; ++b) local += ((cnt[b] + bs - 1) / bs) * bs;
+  for (int b = lo; b < hi; ++b) local += d.pad(cnt[b]);
   const int incl = wave_incl_scan(local);
   int run = incl - local;
   for (int b = lo; b < hi; ++b) {
     cum[b] = run;
-    run += ((cnt[b] + bs - 1) / bs) * bs;
+    run += d.pad(cnt[b]);
   }
   if (lane == kWave - 1) cum[nb] = incl;
 }
 
-__device__ __forceinline__ void fill_eids(const int* cum, int nb, int bs, int NB, int* eids) {
-  for (int b = __lane_id(); b < nb; b += kWave)
-    for (int q = cum[b] / bs; q < cum[b + 1] / bs && q < NB; ++q) eids[q] = b;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// dst[from, to) = v over the wave; 16-byte stores when dst is 16-byte aligned.
+__device__ __forceinline__ void fill_i32(int* dst, int from, int to, int v) {
+  const int lane = __lane_id();
+  if (from >= to) return;
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    const int a0 = min((from + 3) & ~3, to);
+    const int a1 = a0 + ((to - a0) & ~3);
+    if (from + lane < a0) dst[from + lane] = v;
+    for (int p = a0 + 4 * lane; p < a1; p += 4 * kWave)
+      *reinterpret_cast<i32x4*>(dst + p) = i32x4{v, v, v, v};
+    if (a1 + lane < to) dst[a1 + lane] = v;
+  } else {
+    for (int p = from + lane; p < to; p += kWave) dst[p] = v;
+  }
+}
+
+// dst[0, n) = src[0, n) from 16-byte aligned LDS; 16-byte stores when dst is aligned.
+__device__ __forceinline__ void copy_out(int* dst, const int* src, int n) {
+  const int lane = __lane_id();
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    const int n4 = n & ~3;
+    for (int p = 4 * lane; p < n4; p += 4 * kWave)
+      *reinterpret_cast<i32x4*>(dst + p) = *reinterpret_cast<const i32x4*>(src + p);
+    if (n4 + lane < n) dst[n4 + lane] = src[n4 + lane];
+  } else {
+    for (int p = lane; p < n; p += kWave) dst[p] = src[p];
+  }
+}
+
+// Expert id of every block of every non-empty bucket.
+__device__ __forceinline__ void fill_eids(const int* cum, int nb, BlockDiv d, int NB,
+                                          int* eids) {
+  for (int b = __lane_id(); b < nb; b += kWave) {
+    const int q1 = min(d.div(cum[b + 1]), NB);
+    for (int q = d.div(cum[b]); q < q1; ++q) eids[q] = b;
+  }
+}
+
+// Places each routing id at its bucket's cursor plus its rank among the earlier ids of the
+// same bucket in its block of 64, so every bucket is in token order. The lanes of a block
+// sharing a bucket are found by an atomic OR of lane bits into the bucket's mask (order-
+// free, so deterministic); a lane's rank is the popcount of the mask below it.
+__device__ __forceinline__ void place_ids(const ManageArgs& a, const AlignArgs& g,
+                                          const ManageLds<false>& L, AlignLds& A,
+                                          int* sorted_hot, int* sorted_cold) {
+  const int lane = __lane_id();
+  const int E = a.E, S = a.S, mk = a.mk;
+  const int* ids = reinterpret_cast<const int*>(a.ids);
+  for (int base = 0; base < mk; base += kWave) {
+    const int i = base + lane;
+    const int k = i < mk ? align_key(ids[i], E, S, L.tab) : -1;
+    const int kk = k < 0 ? 0 : k;
+    if (k >= 0) A.lanes[kk] = 0;
+    lds_sync();
+    if (k >= 0) atomicOr(&A.lanes[kk], 1ull << lane);
+    lds_sync();
+    int* cur = k >= kMaxSlots ? &A.cur_c[kk - kMaxSlots] : &A.cur_h[kk];
+    const unsigned long long m = A.lanes[kk];
+    const int c0 = *cur;
+    if (k >= 0) {
+      const int before = __popcll(m & lanes_below());
+      const int pos = c0 + before;
+      int* sorted = k >= kMaxSlots ? sorted_cold : sorted_hot;
+      if (pos < g.L) sorted[pos] = i;
+      if ((m >> lane) == 1ull) *cur = c0 + __popcll(m);  // the bucket's last lane moves it
+    }
+    lds_sync();
+  }
 }
 
 __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs& g,
                                            const ManageLds<false>& L, AlignLds& A) {
   const int lane = __lane_id();
-  const int E = a.E, S = a.S, mk = a.mk, bs = g.bs;
+  const int E = a.E, S = a.S, mk = a.mk;
+  const BlockDiv d(g.bs);
   const int* ids = reinterpret_cast<const int*>(a.ids);
 
-  for (int i = lane; i < g.L; i += kWave) {
-    g.sorted_hot[i] = mk;
-    g.sorted_cold[i] = mk;
-  }
-  for (int i = lane; i < g.NB; i += kWave) {
-    g.eids_hot[i] = -1;
-    g.eids_cold[i] = -1;
-  }
   for (int b = lane; b < S; b += kWave) A.cur_h[b] = 0;
   for (int b = lane; b < E; b += kWave) A.cur_c[b] = 0;
   lds_sync();
-
   for (int i = lane; i < mk; i += kWave) {
     const int k = align_key(ids[i], E, S, L.tab);
     if (k >= kMaxSlots)
@@ -85,38 +163,48 @@ __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs&
       atomicAdd(&A.cur_h[k], 1);
   }
   lds_sync();
-  padded_scan(A.cur_h, A.cum_h, S, bs);
-  padded_scan(A.cur_c, A.cum_c, E, bs);
+  padded_scan(A.cur_h, A.cum_h, S, d);
+  padded_scan(A.cur_c, A.cum_c, E, d);
   lds_sync();
+  const int tot_h = A.cum_h[S], tot_c = A.cum_c[E];
   if (lane == 0) {
-    g.npad_hot[0] = A.cum_h[S];
-    g.npad_cold[0] = A.cum_c[E];
+    g.npad_hot[0] = tot_h;
+    g.npad_cold[0] = tot_c;
   }
   for (int b = lane; b < S; b += kWave) A.cur_h[b] = A.cum_h[b];
   for (int b = lane; b < E; b += kWave) A.cur_c[b] = A.cum_c[b];
-  mem_sync();  // the defaults above are written before any real entry lands on them
 
-  fill_eids(A.cum_h, S, bs, g.NB, g.eids_hot);
-  fill_eids(A.cum_c, E, bs, g.NB, g.eids_cold);
-
-  for (int base = 0; base < mk; base += kWave) {
-    const int i = base + lane;
-    const int k = i < mk ? align_key(ids[i], E, S, L.tab) : -1;
-    int before = 0, after = 0;
-    for (int jl = 0; jl < kWave; ++jl) {
-      const int kj = wave_lane_value(k, jl);
-      before += (kj == k && jl < lane);
-      after += (kj == k && jl > lane);
-    }
-    int* cur = k >= kMaxSlots ? &A.cur_c[k - kMaxSlots] : &A.cur_h[k < 0 ? 0 : k];
-    if (k >= 0) {
-      const int pos = *cur + before;
-      int* sorted = k >= kMaxSlots ? g.sorted_cold : g.sorted_hot;
-      if (pos < g.L) sorted[pos] = i;
-    }
+  // Every position below a side's padded total is an id or its bucket's padding, every
+  // block below it belongs to a bucket; past it the outputs hold mk and -1.
+  const int nh = min(tot_h, g.L), nc = min(tot_c, g.L);
+  const int qh = min(d.div(tot_h), g.NB), qc = min(d.div(tot_c), g.NB);
+  const int oh = (nh + 3) & ~3, oc = (nc + 3) & ~3;
+  if (oh + qh <= kStage && oc + qc <= kStage) {
+    int* sh = A.stage[0];
+    int* sc = A.stage[1];
+    fill_i32(sh, 0, nh, mk);
+    fill_i32(sc, 0, nc, mk);
+    fill_eids(A.cum_h, S, d, g.NB, sh + oh);
+    fill_eids(A.cum_c, E, d, g.NB, sc + oc);
+    fill_i32(g.sorted_hot, nh, g.L, mk);
+    fill_i32(g.sorted_cold, nc, g.L, mk);
+    fill_i32(g.eids_hot, qh, g.NB, -1);
+    fill_i32(g.eids_cold, qc, g.NB, -1);
     lds_sync();
-    if (k >= 0 && after == 0) *cur += before + 1;
-    lds_sync();
+    place_ids(a, g, L, A, sh, sc);  // ends with an LDS sync
+    copy_out(g.sorted_hot, sh, nh);
+    copy_out(g.eids_hot, sh + oh, qh);
+    copy_out(g.sorted_cold, sc, nc);
+    copy_out(g.eids_cold, sc + oc, qc);
+  } else {
+    fill_i32(g.sorted_hot, 0, g.L, mk);
+    fill_i32(g.eids_hot, 0, g.NB, -1);
+    fill_i32(g.sorted_cold, 0, g.L, mk);
+    fill_i32(g.eids_cold, 0, g.NB, -1);
+    mem_sync();  // the defaults are written before any entry below lands on them
+    fill_eids(A.cum_h, S, d, g.NB, g.eids_hot);
+    fill_eids(A.cum_c, E, d, g.NB, g.eids_cold);
+    place_ids(a, g, L, A, g.sorted_hot, g.sorted_cold);
   }
 }
 

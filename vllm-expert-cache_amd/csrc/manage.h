@@ -58,9 +58,8 @@ struct ManageLds {
   alignas(16) unsigned char flag[GLOBAL_E ? 16 : kLdsExperts];  // cleared 16 bytes a lane
   alignas(16) unsigned char hit[kMaxSlots];  // slot refreshed by a routed expert this step
   int tab[GLOBAL_E ? 1 : kLdsExperts];
-  int se[kMaxSlots];               // slot -> expert, for the installs
   alignas(16) long long key[kMaxSlots + 8];  // select path: victim keys, INT64_MAX padded
-  int vic[kMaxInserts];            // insert r -> victim slot
+  int rank[kMaxSlots];             // select path: key order of each compacted victim
   int mis[kMaxInserts];            // insert r -> missing expert
 };
 
@@ -92,13 +91,14 @@ __device__ __forceinline__ long long victim_key(long long stamp, int slot) {
   return (long long)(((unsigned long long)stamp << kSlotBits) | (unsigned long long)slot);
 }
 
-// Which victim search is cheaper: a wave-min reduction plus its install per insert, or
-// the threshold select (a fixed cost of about two wave-min reductions, ~20 ballot-count
-// probes and one parallel install pass).
+// Which victim search is cheaper: a wave-min reduction plus its install per insert
+// (measured on gfx950: ~0.27 us per insert with one slot per lane, ~0.3-0.6 us with 2-8),
+// or the threshold select, whose cost hardly depends on the insert count (~1.3 us with one
+// slot per lane, ~2-3.6 us with 2-8). The crossovers are about 3 and 6 inserts.
 template <int CS>
 __device__ __forceinline__ bool use_argmin(int nact, int nev) {
   (void)nev;
-  return nact <= (CS <= 2 ? 2 : 3);
+  return nact <= (CS == 1 ? 3 : 6);
 }
 
 __device__ __forceinline__ long long uniform_i64(long long v) {
@@ -455,12 +455,12 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
           rank += (k01.x < kj) + (k01.y < kj) + (k23.x < kj) + (k23.y < kj) + (k45.x < kj) +
                   (k45.y < kj) + (k67.x < kj) + (k67.y < kj);
         }
-        if (j < nbelow) L.vic[j] = rank;
+        if (j < nbelow) L.rank[j] = rank;
       }
       lds_sync();
 #pragma unroll
       for (int c = 0; c < CS; ++c)
-        if (below[c]) pos[c] = L.vic[pos[c]];
+        if (below[c]) pos[c] = L.rank[pos[c]];
     }
 
     // installs, each by the lane holding the victim slot
