@@ -80,3 +80,33 @@ def test_random_shapes(seed):
             assert np.array_equal(got, want), f"{tag}: {name} differs at {gu.first_diff(got, want)}"
         if fused_remap and mk:
             assert np.array_equal(out.cpu().numpy()[:mk], oracle.remap(ids, ref.table)), tag
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_extreme_stamps(seed):
+    """Warm states whose stamps spread over more than 2^31 (and whose keys overflow the
+    20-bit shift, some negative), with enough misses per step for the many-insert search:
+    its 64-bit form runs here, against the oracle's rank rule on every field."""
+    rng = np.random.default_rng(1000 + seed)
+    E = int(rng.choice([300, 1000, 4096]))
+    S = int(rng.choice([65, 200, 257, 1024]))
+    mk, mi = int(rng.choice([64, 200, 256])), S
+    nhot = min(S, E) - int(rng.integers(0, 8))
+    hot = rng.choice(E, nhot, replace=False)
+    slots = rng.choice(S, nhot, replace=False)
+    lo, hi = [(-(1 << 62), 1 << 62), (0, 1 << 45), (1 << 40, (1 << 40) + (1 << 33))][seed % 3]
+    stamps = rng.integers(lo, hi, size=S)
+    st, ref = _device_state(E, S, mi, hot, slots, stamps)
+    policy, decay = seed % 2, int(rng.choice([0, 3]))
+    for t in range(6):
+        ids = rng.integers(0, E, size=mk).astype(np.int32)
+        d_ids = torch.as_tensor(ids, device=gu.DEV)
+        assert gu.manage_call(gu.lib(), st, 0, gu.ptr(d_ids), mk, mk, mi, policy, decay) == 0
+        assert ref.manage(ids, mk, mi, policy, decay) == 0
+        torch.cuda.synchronize()
+        tag = f"seed {seed} step {t}: E={E} S={S} mk={mk} pol={policy} dec={decay} n_miss={ref.n_miss}"
+        for name, dev in (("table", st.table[0]), ("map_cold", st.map_cold[0]),
+                          ("slot_expert", st.slot_expert[0]), ("slot_stamp", st.slot_stamp[0]),
+                          ("step", st.step[0]), ("miss", st.miss[0]), ("n_miss", st.n_miss[0])):
+            got, want = dev.cpu().numpy(), getattr(ref, name)
+            assert np.array_equal(got, want), f"{tag}: {name} differs at {gu.first_diff(got, want)}"
