@@ -96,7 +96,7 @@ int expert_cache_remap(const void* ids, int n, int id_bytes, const int* table, i
  * table, in one launch. `ids` are int32 (id_bytes 4) or int64 (id_bytes 8); the policy sees
  * each id truncated to int32, as the reference's `topk_ids.to(torch.int32)` does, and `out`
  * receives the slot ids in the dtype of `ids`. Argument checks are those of
- * expert_cache_manage plus id_bytes in {4, 8}.
+ * expert_cache_manage plus id_bytes in {4, 8} and out non-null when mk > 0.
  *
  * Replaces: vllm_expert_cache/cache.py:116-133 plus :163 (cast, manage, and the torch
  * remap); no counterpart in the reference's C-ABI.

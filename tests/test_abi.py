@@ -129,6 +129,8 @@ def test_manage_remap_rejects(lib):
         a = dict(base, **{k: v})
         assert fn(P(1), a["id_bytes"], 1, a["E"], a["S"], 1, a["mi"], *([P(1)] * 8), a["pol"],
                   64, P(1), None) == -1, (k, v)
+    # ids to remap but nowhere to put them
+    assert fn(P(1), 4, 1, 8, 4, 1, 4, *([P(1)] * 8), 0, 64, None, None) == -1
 
 
 def test_remap_rejects_and_empty_is_a_no_op(lib):

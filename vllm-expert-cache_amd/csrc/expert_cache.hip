@@ -114,6 +114,7 @@ int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int 
                               void* out, hipStream_t stream) {
   if (manage_args_bad(E, S, max_inserts, policy)) return -1;
   if (id_bytes != 4 && id_bytes != 8) return -1;
+  if (mk > 0 && out == nullptr) return -1;
   const ManageArgs a = make_args(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
                                  slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
                                  decay, out);
