@@ -193,6 +193,10 @@ int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void*
     g.vec[b] = 0;
     g.tile0[b + 1] = g.tile0[b];
   }
+  g.per = g.tile0[g.nbuf];
+  const long long nblk = (long long)chunks * lanes;
+  g.jstep = g.per > 0 ? nblk / g.per : 0;
+  g.rstep = g.per > 0 ? nblk % g.per : 0;
   hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false>), dim3(chunks, lanes),
                      dim3(kGatherThreads), 0, stream, g, miss, n_miss);
   return (int)hipGetLastError();

@@ -24,6 +24,9 @@ struct GatherArgs {
   const u32x4* src[kGatherBufs];
   long long vec[kGatherBufs];            // 16-byte vectors per expert
   long long tile0[kGatherBufs + 1];      // first tile of buffer b within one miss
+  long long per;                         // tiles per miss (tile0[nbuf])
+  long long jstep, rstep;                // a workgroup's stride in (miss, tile): grid / per,
+                                         // grid % per (computed by the host)
   int nbuf;                              // distinct buffers after de-duplication
 };
 
@@ -35,17 +38,28 @@ struct GatherTile {
   int n;
 };
 
+// The buffer of tile r and its fields are picked with constant indexes only (a select
+// chain), so every field is a kernel argument the wave loads once, up front.
 template <int U>
 __device__ __forceinline__ GatherTile gather_tile(const GatherArgs& g, int e, int sl,
                                                   long long r) {
   constexpr long long kTile = (long long)kGatherThreads * U;
-  int b = 0;
-  while (b + 1 < g.nbuf && r >= g.tile0[b + 1]) ++b;
-  const long long V = g.vec[b];
-  const long long off = (r - g.tile0[b]) * kTile;
+  const u32x4* src = g.src[0];
+  u32x4* dst = g.dst[0];
+  long long V = g.vec[0], first = g.tile0[0];
+#pragma unroll
+  for (int i = 1; i < kGatherBufs; ++i) {
+    if (i < g.nbuf && r >= g.tile0[i]) {
+      src = g.src[i];
+      dst = g.dst[i];
+      V = g.vec[i];
+      first = g.tile0[i];
+    }
+  }
+  const long long off = (r - first) * kTile;
   GatherTile t;
-  t.src = g.src[b] + (long long)e * V + off;
-  t.dst = g.dst[b] + (long long)sl * V + off;
+  t.src = src + (long long)e * V + off;
+  t.dst = dst + (long long)sl * V + off;
   t.n = (int)min(kTile, V - off);
   return t;
 }
@@ -86,15 +100,21 @@ template <int U, bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
                                                            const int* __restrict__ miss,
                                                            const int* __restrict__ n_miss) {
-  const long long per = g.tile0[g.nbuf];
+  const long long per = g.per;
   const long long nblk = (long long)gridDim.x * gridDim.y;
   const long long t0 = (long long)blockIdx.y * gridDim.x + blockIdx.x;
-  const int nm = n_miss[0];
+  // The first miss pair is read together with n_miss (the miss list always holds one
+  // pair): when this workgroup's first tile is in miss 0 -- every workgroup, once an expert
+  // spans more tiles than the grid has workgroups -- no second round trip is needed.
+  int nm = n_miss[0], e0 = miss[0], sl0 = miss[1];
+  // nothing may use the three values before this point: their loads go out together
+  asm volatile("" : "+s"(nm), "+s"(e0), "+s"(sl0));
   if (nm <= 0 || per <= 0 || t0 >= (long long)nm * per) return;
-  const long long jstep = nblk / per, rstep = nblk % per;
-  int j = (int)(t0 / per);
+  const long long jstep = g.jstep, rstep = g.rstep;
+  // first tile: in miss 0 whenever a miss spans more tiles than the grid has workgroups
+  int j = t0 < per ? 0 : (int)(t0 / per);
   long long r = t0 - (long long)j * per;
-  int e = miss[2 * j], sl = miss[2 * j + 1];
+  int e = j == 0 ? e0 : miss[2 * j], sl = j == 0 ? sl0 : miss[2 * j + 1];
   GatherTile cur = gather_tile<U>(g, e, sl, r);
   u32x4 v[U];
   tile_load<U, NT_LOAD>(cur, v);
