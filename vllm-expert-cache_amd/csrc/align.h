@@ -208,13 +208,13 @@ __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs&
   }
 }
 
-template <int CS>
+template <int CS, int TQ>
 __global__ __launch_bounds__(kWave) void fused_k(ManageArgs a, AlignArgs g) {
   __shared__ ManageLds<false> L;
   __shared__ AlignLds A;
   args_in_sgprs(a);
   long long idv[kIdRegs];
-  manage_step<CS, false, 4>(a, L, idv);
+  manage_step<CS, false, 4, TQ>(a, L, idv);
   lds_sync();
   align_tail(a, g, L, A);
 }

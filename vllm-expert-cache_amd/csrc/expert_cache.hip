@@ -30,38 +30,62 @@ bool manage_args_bad(int E, int S, int max_inserts, int policy) {
   return false;
 }
 
-template <int IDB, bool REMAP>
-int launch_manage(const ManageArgs& a, hipStream_t stream) {
+// Slots per lane (CS) by S, and table chunks held in registers (TQ) by E.
+template <int IDB, bool REMAP, int TQ>
+int launch_manage_tq(const ManageArgs& a, hipStream_t stream) {
   const dim3 grid(1), block(kWave);
-  if (a.E > kLdsExperts) {
-    hipLaunchKernelGGL((manage_k<16, true, IDB, REMAP>), grid, block, 0, stream, a);
-  } else if (a.S <= 64) {
-    hipLaunchKernelGGL((manage_k<1, false, IDB, REMAP>), grid, block, 0, stream, a);
+  if (a.S <= 64) {
+    hipLaunchKernelGGL((manage_k<1, false, IDB, REMAP, TQ>), grid, block, 0, stream, a);
   } else if (a.S <= 128) {
-    hipLaunchKernelGGL((manage_k<2, false, IDB, REMAP>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((manage_k<2, false, IDB, REMAP, TQ>), grid, block, 0, stream, a);
   } else if (a.S <= 256) {
-    hipLaunchKernelGGL((manage_k<4, false, IDB, REMAP>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((manage_k<4, false, IDB, REMAP, TQ>), grid, block, 0, stream, a);
   } else if (a.S <= 512) {
-    hipLaunchKernelGGL((manage_k<8, false, IDB, REMAP>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((manage_k<8, false, IDB, REMAP, TQ>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL((manage_k<16, false, IDB, REMAP>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((manage_k<16, false, IDB, REMAP, TQ>), grid, block, 0, stream, a);
   }
   return (int)hipGetLastError();
 }
 
-int launch_fused(const ManageArgs& a, const AlignArgs& g, hipStream_t stream) {
+template <int IDB, bool REMAP>
+int launch_manage(const ManageArgs& a, hipStream_t stream) {
+  if (a.E > kLdsExperts) {
+    hipLaunchKernelGGL((manage_k<16, true, IDB, REMAP, kTabRegs>), dim3(1), dim3(kWave), 0,
+                       stream, a);
+    return (int)hipGetLastError();
+  }
+  switch (table_chunks(a.E)) {
+    case 1: return launch_manage_tq<IDB, REMAP, 1>(a, stream);
+    case 2: return launch_manage_tq<IDB, REMAP, 2>(a, stream);
+    case 4: return launch_manage_tq<IDB, REMAP, 4>(a, stream);
+    default: return launch_manage_tq<IDB, REMAP, kTabRegs>(a, stream);
+  }
+}
+
+template <int TQ>
+int launch_fused_tq(const ManageArgs& a, const AlignArgs& g, hipStream_t stream) {
   const dim3 grid(1), block(kWave);
   if (a.S <= 64)
-    hipLaunchKernelGGL((fused_k<1>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((fused_k<1, TQ>), grid, block, 0, stream, a, g);
   else if (a.S <= 128)
-    hipLaunchKernelGGL((fused_k<2>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((fused_k<2, TQ>), grid, block, 0, stream, a, g);
   else if (a.S <= 256)
-    hipLaunchKernelGGL((fused_k<4>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((fused_k<4, TQ>), grid, block, 0, stream, a, g);
   else if (a.S <= 512)
-    hipLaunchKernelGGL((fused_k<8>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((fused_k<8, TQ>), grid, block, 0, stream, a, g);
   else
-    hipLaunchKernelGGL((fused_k<16>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((fused_k<16, TQ>), grid, block, 0, stream, a, g);
   return (int)hipGetLastError();
+}
+
+int launch_fused(const ManageArgs& a, const AlignArgs& g, hipStream_t stream) {
+  switch (table_chunks(a.E)) {
+    case 1: return launch_fused_tq<1>(a, g, stream);
+    case 2: return launch_fused_tq<2>(a, g, stream);
+    case 4: return launch_fused_tq<4>(a, g, stream);
+    default: return launch_fused_tq<kTabRegs>(a, g, stream);
+  }
 }
 
 ManageArgs make_args(const void* ids, int mk, int E, int S, int max_distinct, int max_inserts,

@@ -33,7 +33,7 @@ constexpr int kMaxSlots = 1024;
 constexpr int kMaxInserts = 1024;
 constexpr int kLdsExperts = 4096;   // flags + table fit in LDS up to this many experts
 constexpr int kIdRegs = 4;          // ids held in registers: mk <= 256
-constexpr int kTabRegs = 8;         // table entries prefetched per lane: E <= 512
+constexpr int kTabRegs = 8;         // most table entries held per lane: E <= 512
 constexpr long long kKeyMax = 0x7FFFFFFFFFFFFFFFll;
 
 struct ManageArgs {
@@ -108,9 +108,14 @@ __device__ __forceinline__ long long uniform_i64(long long v) {
   return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
+// Table chunks of 64 experts a lane holds in registers for E experts: the launch picks the
+// smallest of 1, 2, 4, 8 that covers E (8 also above 512 experts, which the general loops
+// handle), so small expert counts do not carry code for 512.
+constexpr int table_chunks(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
+
 // One policy step. On return, the updated table is in L.tab (or in memory for GLOBAL_E)
-// and idv holds ids[lane + 64k] (or -1 past mk).
-template <int CS, bool GLOBAL_E, int IDB>
+// and idv holds ids[lane + 64k] (or -1 past mk). TQ table chunks are held in registers.
+template <int CS, bool GLOBAL_E, int IDB, int TQ>
 __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBAL_E>& L,
                                             long long (&idv)[kIdRegs]) {
   const int lane = __lane_id();
@@ -139,10 +144,10 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     se[c] = a.slot_expert[s];
     sp[c] = a.slot_stamp[s];
   }
-  int tv[kTabRegs];
+  int tv[TQ];
   if constexpr (!GLOBAL_E) {
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) tv[u] = a.table[min(lane + u * kWave, E - 1)];
+    for (int u = 0; u < TQ; ++u) tv[u] = a.table[min(lane + u * kWave, E - 1)];
   }
   unsigned char* flag;
   if constexpr (GLOBAL_E)
@@ -183,8 +188,8 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   if constexpr (!GLOBAL_E) {
     // entries past E (below 512) are written too: nothing reads them
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) L.tab[lane + u * kWave] = tv[u];
-    for (int base = kTabRegs * kWave; base < E; base += kTabRegs * kWave) {
+    for (int u = 0; u < TQ; ++u) L.tab[lane + u * kWave] = tv[u];
+    for (int base = TQ * kWave; base < E; base += kTabRegs * kWave) {
       int tw[kTabRegs];
 #pragma unroll
       for (int u = 0; u < kTabRegs; ++u) tw[u] = a.table[min(base + lane + u * kWave, E - 1)];
@@ -200,18 +205,18 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   // ---- distinct count (the caller's `routed` is left holding the flags), then hits mark
   // ---- their slot and misses enumerate in ascending expert id ------------------------
   int cnt = 0, total = 0;
-  if (!GLOBAL_E && E <= kTabRegs * kWave) {
+  if (!GLOBAL_E && E <= TQ * kWave) {
     // the whole table is in registers: one batch of flag reads, no table re-read; chunks
     // past E are skipped on a uniform branch
     const int nchunk = (E + kWave - 1) / kWave;
-    unsigned char fb[kTabRegs];
-    bool fl[kTabRegs];
+    unsigned char fb[TQ];
+    bool fl[TQ];
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) fb[u] = flag[min(lane + u * kWave, E - 1)];
+    for (int u = 0; u < TQ; ++u) fb[u] = flag[min(lane + u * kWave, E - 1)];
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) fl[u] = (fb[u] != 0) & (lane + u * kWave < E);
+    for (int u = 0; u < TQ; ++u) fl[u] = (fb[u] != 0) & (lane + u * kWave < E);
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) {
+    for (int u = 0; u < TQ; ++u) {
       if (u < nchunk) {
         // lanes past E store routed[E-1]'s own flag there: no store needs a branch
         a.routed[min(lane + u * kWave, E - 1)] = fb[u] != 0 ? 1 : 0;
@@ -226,7 +231,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       return;
     }
 #pragma unroll
-    for (int u = 0; u < kTabRegs; ++u) {
+    for (int u = 0; u < TQ; ++u) {
       if (u < nchunk) {
         const int e = lane + u * kWave;
         const int t = tv[u];
@@ -536,12 +541,12 @@ __device__ __forceinline__ void args_in_sgprs(const ManageArgs& a) {
                "s"(a.max_inserts), "s"(a.policy), "s"(a.decay));
 }
 
-template <int CS, bool GLOBAL_E, int IDB, bool REMAP>
+template <int CS, bool GLOBAL_E, int IDB, bool REMAP, int TQ>
 __global__ __launch_bounds__(kWave) void manage_k(ManageArgs a) {
   __shared__ ManageLds<GLOBAL_E> L;
   args_in_sgprs(a);
   long long idv[kIdRegs];
-  manage_step<CS, GLOBAL_E, IDB>(a, L, idv);
+  manage_step<CS, GLOBAL_E, IDB, TQ>(a, L, idv);
   if constexpr (REMAP) {
     if constexpr (GLOBAL_E) mem_sync();
     else lds_sync();
