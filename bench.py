@@ -79,8 +79,9 @@ def parse():
 
 
 def traffic_probe(args):
-    """Known work for the FETCH_SIZE / WRITE_SIZE counter runs: the counter value of the
-    plain copy per byte calibrates the gather's per-launch counter into bytes."""
+    """Known work for the counter runs: 16 one-expert gathers, 128 policy+remap steps of one
+    layer, and 8 plain device copies whose FETCH_SIZE / WRITE_SIZE per byte calibrate the
+    kernels' per-launch counters into bytes."""
     import torch
 
     from vllm_expert_cache import _lib, traces
@@ -106,6 +107,20 @@ def traffic_probe(args):
                                      ctypes.c_void_p(one.data_ptr()), args.chunks or
                                      DEFAULT_CHUNKS, args.lanes or DEFAULT_LANES, s_ptr)
         assert rc == 0
+    # policy+remap: 128 decode steps of the workload's layer 0 from a cold start (the
+    # counters of the last 64 are the steady state)
+    mk = w.mk
+    ids = torch.as_tensor(traces.routing(w, 0, 128), device=dev)
+    st = Layers(torch, 1, E, S, dev)
+    nm = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.zeros(mk, dtype=torch.int32, device=dev)
+    for t in range(128):
+        rc = lib.expert_cache_manage_remap(
+            ctypes.c_void_p(ids[t].data_ptr()), 4, mk, E, S, min(E, mk), S, st.row("table", 0),
+            st.row("map_cold", 0), st.row("slot_expert", 0), st.row("slot_stamp", 0),
+            st.row("routed", 0), st.row("step", 0), st.row("miss", 0),
+            ctypes.c_void_p(nm.data_ptr()), 1, 64, ctypes.c_void_p(out.data_ptr()), s_ptr)
+        assert rc == 0
     n = 64 << 20
     src = torch.ones(n, dtype=torch.uint8, device=dev)
     dst = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -113,7 +128,8 @@ def traffic_probe(args):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"gather_launches": 16, "gather_bytes_per_launch": sum(bufs),
-                      "copy_launches": 8, "copy_bytes_per_launch": n}), flush=True)
+                      "manage_remap_launches": 128, "copy_launches": 8,
+                      "copy_bytes_per_launch": n}), flush=True)
 
 
 class Layers:
@@ -417,6 +433,7 @@ def main():
         "manage_remap_us_per_layer": manage_us,
         "manage_remap_def": manage_def,
         "manage_remap_us_per_layer_events": round(float(man_us.mean()), 3),
+        "manage_remap_counters": _manage_counters(),
         "gather_us_per_launch": round(float(gat_us.mean()), 3),
         "gather_GBps_launches_with_miss": None if per_miss is None else round(per_miss, 3),
         "link_peak_GBps": {"hipMemcpyAsync_h2d": round(memcpy_gbps, 3),
@@ -580,6 +597,20 @@ def _traffic():
             "write_bytes_per_miss": t["write_bytes_per_launch"],
             "algorithmic_bytes_per_miss": t["algorithmic_bytes_per_launch"],
             "fetch_over_algorithmic": t["fetch_over_algorithmic"],
+            "source": f"profiles/{p.name}"}
+
+
+def _manage_counters():
+    """Hardware counters per policy+remap call (rocprofv3, calibrated), from the committed
+    profile summary; None if absent."""
+    p = ROOT / "profiles" / "manage_k-counters-48-layer-e128.json"
+    try:
+        t = json.loads(p.read_text())["per_call"]
+    except (OSError, ValueError, KeyError):
+        return None
+    return {"hbm_bytes_read": t["hbm_fetch_bytes"], "hbm_bytes_written": t["hbm_write_bytes"],
+            "hbm_GBps": t["hbm_GBps"], "lds_instructions": t["SQ_INSTS_LDS"],
+            "lds_GBps_estimate": t["lds_GBps_estimate"], "duration_us": t["duration_us"],
             "source": f"profiles/{p.name}"}
 
 
