@@ -107,6 +107,28 @@ int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int 
                               long long* step, int* miss, int* n_miss, int policy, int decay,
                               void* out, hipStream_t stream);
 
+/*
+ * Prefetch step: bring the experts predicted for this layer's next step into slots ahead of
+ * that step, so their copy can run (expert_cache_gather over this call's miss list, on any
+ * stream) while other work proceeds. It installs like expert_cache_manage -- the predicted
+ * experts that are not resident, in ascending id order, into the lowest (stamp, slot) keys
+ * among the slots whose expert is not predicted, at most max_inserts of them, writing the
+ * (expert, slot) pairs to miss and their count to n_miss -- but it does not advance any step
+ * counter, leaves the stamps of resident predicted experts alone, never ages, and gives each
+ * install stamp 0. An unused prediction is therefore the first victim of the next real step,
+ * and a right prediction leaves the policy state after the next expert_cache_manage equal to
+ * what that call alone would give (except on an LFU step that would have aged the counts).
+ * `routed` is left holding the predicted flags. pred_ids are int32; ids outside [0, E) are
+ * ignored. Use a miss/n_miss pair of its own, not the one the real step's gather reads.
+ * Fails with -1 unless E > 0, 0 < S <= 1024, 0 <= max_inserts <= 1024 and mk >= 0.
+ *
+ * No counterpart in the reference's C-ABI: README.md:392-394 names next-layer prefetch as
+ * the path's next step without implementing it.
+ */
+int expert_cache_prefetch(const int* pred_ids, int mk, int E, int S, int max_inserts,
+                          int* table, int* map_cold, int* slot_expert, long long* slot_stamp,
+                          unsigned char* routed, int* miss, int* n_miss, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,8 @@ def lib():
         h.oracle_run_trace.argtypes = [_P, _I, _I, _I, _I, _I, _I, _I] + [_P] * 11
         h.oracle_now.restype = ctypes.c_double
         h.oracle_now.argtypes = []
+        h.oracle_prefetch.restype = _I
+        h.oracle_prefetch.argtypes = [_P, _I, _I, _I, _I] + [_P] * 7 + [_I]
         h.oracle_fused.restype = _I
         h.oracle_fused.argtypes = ([_P, _I, _I, _I, _I, _I] + [_P] * 8 + [_I, _I, _I]
                                    + [_P] * 6)
@@ -95,6 +97,14 @@ class State:
                  int(max_inserts), _ptr(self.table), _ptr(self.map_cold),
                  _ptr(self.slot_expert), _ptr(self.slot_stamp), _ptr(self.routed),
                  _ptr(self.step), _ptr(self.miss), _ptr(self.n_miss), int(policy), int(decay))
+
+    def prefetch(self, ids, max_inserts: int, rule: str = "rank") -> int:
+        """Install-only step for predicted ids (stamp 0, step and hit stamps untouched)."""
+        ids = np.ascontiguousarray(np.asarray(ids).ravel().astype(np.int32))
+        return lib().oracle_prefetch(
+            _ptr(ids), int(ids.size), self.E, self.S, int(max_inserts), _ptr(self.table),
+            _ptr(self.map_cold), _ptr(self.slot_expert), _ptr(self.slot_stamp),
+            _ptr(self.routed), _ptr(self.miss), _ptr(self.n_miss), 0 if rule == "serial" else 1)
 
     def fused(self, ids, max_distinct: int, max_inserts: int, bs: int, L: int, NB: int):
         ids = np.ascontiguousarray(np.asarray(ids).ravel().astype(np.int32))

@@ -17,6 +17,8 @@
  *   gather                kernels/expert_cache.hip:284-314 (byte copy of each miss's slabs)
  *   fused align           kernels/expert_cache.hip:431-588 (LRU manage + both
  *                                                            moe_align_block_size outputs)
+ *   prefetch              README.md:392-394 names next-layer prefetch; its install-only
+ *                         step is defined below and pinned against the manage rules
  *
  * Two independent victim rules (serial argmin, batched rank-select) are kept on purpose: the
  * reference argues they are the same answer (kernels/expert_cache.hip:83-97) and the tests
@@ -183,6 +185,83 @@ int oracle_manage_rank(const int32_t* ids, int mk, int E, int S, int max_distinc
   const int nact = nins < nev ? nins : nev;
   for (int r = 0; r < nact; r++)
     install(r, vic[r], misses[r], fresh, E, table, map_cold, slot_expert, slot_stamp, miss);
+  n_miss[0] = nact;
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Prefetch: the install-only step that brings a layer's predicted experts in ahead of its
+ * next real step (README.md:392-394 names the idea; the reference has no implementation, so
+ * these rules are this library's own and are pinned by tests against the manage rules):
+ *   - n_miss = 0; `routed` is left holding the predicted flags (ids outside [0,E) ignored);
+ *   - the step counter does not move, resident predicted experts keep their stamps, no decay;
+ *   - the predicted experts that are not resident, in ascending id order, are the misses;
+ *     nins = min(misses, max_inserts), miss[2j] = misses[j] for j < nins;
+ *   - victims are the nins smallest keys stamp<<20 | slot among the slots whose expert is not
+ *     predicted, exactly as in manage; each install gets stamp 0, below every stamp a real
+ *     step gives, so a wrong prediction is the first victim afterwards, and a right one's
+ *     first real hit gives it the stamp a real install would have (st under LRU, 1 under
+ *     LFU).
+ * Consequence, checked by the tests: with the prediction equal to the next step's routed set,
+ * prefetch followed by manage leaves the same state as manage alone, with the miss list
+ * moved to the prefetch, whenever that manage step would not decay.
+ * `rule` 0 = serial argmin, 1 = rank.
+ * ------------------------------------------------------------------------------------- */
+int oracle_prefetch(const int32_t* ids, int mk, int E, int S, int max_inserts, int32_t* table,
+                    int32_t* map_cold, int32_t* slot_expert, int64_t* slot_stamp,
+                    uint8_t* routed, int32_t* miss, int32_t* n_miss, int rule) {
+  if (manage_args_bad(E, S, max_inserts, 0) || mk < 0) return -1;
+  n_miss[0] = 0;
+  memset(routed, 0, (size_t)E);
+  for (int i = 0; i < mk; i++) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) routed[e] = 1;
+  }
+  int32_t misses[OR_MAXINS];
+  int total = 0;
+  for (int e = 0; e < E; e++) {
+    if (!routed[e] || table[e] >= 0) continue;
+    if (total < max_inserts) misses[total] = e;
+    total++;
+  }
+  const int nins = total < max_inserts ? total : max_inserts;
+  for (int j = 0; j < nins; j++) miss[2 * j] = misses[j];
+  if (nins == 0) return 0;
+
+  int nact = 0;
+  if (rule == 0) {
+    for (int r = 0; r < nins; r++) {
+      int best = -1;
+      for (int i = 0; i < S; i++) {
+        if (!slot_evictable(slot_expert, routed, E, i)) continue;
+        if (best < 0 || slot_stamp[i] < slot_stamp[best] ||
+            (slot_stamp[i] == slot_stamp[best] && i < best))
+          best = i;
+      }
+      if (best < 0) break;
+      install(r, best, misses[r], 0, E, table, map_cold, slot_expert, slot_stamp, miss);
+      nact++;
+    }
+  } else {
+    int64_t key[OR_MAXS];
+    uint8_t ev[OR_MAXS];
+    int vic[OR_MAXINS];
+    int nev = 0;
+    for (int i = 0; i < S; i++) {
+      ev[i] = (uint8_t)slot_evictable(slot_expert, routed, E, i);
+      key[i] = vkey(slot_stamp[i], i);
+      nev += ev[i];
+    }
+    for (int i = 0; i < S; i++) {
+      if (!ev[i]) continue;
+      int rank = 0;
+      for (int j = 0; j < S; j++) rank += (ev[j] && key[j] < key[i]);
+      if (rank < nins) vic[rank] = i;
+    }
+    nact = nins < nev ? nins : nev;
+    for (int r = 0; r < nact; r++)
+      install(r, vic[r], misses[r], 0, E, table, map_cold, slot_expert, slot_stamp, miss);
+  }
   n_miss[0] = nact;
   return 0;
 }

@@ -64,6 +64,35 @@ int launch_manage(const ManageArgs& a, hipStream_t stream) {
 }
 
 template <int TQ>
+int launch_prefetch_tq(const ManageArgs& a, hipStream_t stream) {
+  const dim3 grid(1), block(kWave);
+  if (a.S <= 64)
+    hipLaunchKernelGGL((prefetch_k<1, false, TQ>), grid, block, 0, stream, a);
+  else if (a.S <= 128)
+    hipLaunchKernelGGL((prefetch_k<2, false, TQ>), grid, block, 0, stream, a);
+  else if (a.S <= 256)
+    hipLaunchKernelGGL((prefetch_k<4, false, TQ>), grid, block, 0, stream, a);
+  else if (a.S <= 512)
+    hipLaunchKernelGGL((prefetch_k<8, false, TQ>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((prefetch_k<16, false, TQ>), grid, block, 0, stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_prefetch(const ManageArgs& a, hipStream_t stream) {
+  if (a.E > kLdsExperts) {
+    hipLaunchKernelGGL((prefetch_k<16, true, kTabRegs>), dim3(1), dim3(kWave), 0, stream, a);
+    return (int)hipGetLastError();
+  }
+  switch (table_chunks(a.E)) {
+    case 1: return launch_prefetch_tq<1>(a, stream);
+    case 2: return launch_prefetch_tq<2>(a, stream);
+    case 4: return launch_prefetch_tq<4>(a, stream);
+    default: return launch_prefetch_tq<kTabRegs>(a, stream);
+  }
+}
+
+template <int TQ>
 int launch_fused_tq(const ManageArgs& a, const AlignArgs& g, hipStream_t stream) {
   const dim3 grid(1), block(kWave);
   if (a.S <= 64)
@@ -143,6 +172,17 @@ int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int 
                                  slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
                                  decay, out);
   return id_bytes == 8 ? launch_manage<8, true>(a, stream) : launch_manage<4, true>(a, stream);
+}
+
+int expert_cache_prefetch(const int* pred_ids, int mk, int E, int S, int max_inserts,
+                          int* table, int* map_cold, int* slot_expert, long long* slot_stamp,
+                          unsigned char* routed, int* miss, int* n_miss, hipStream_t stream) {
+  if (manage_args_bad(E, S, max_inserts, 0) || mk < 0) return -1;
+  // max_distinct = E: a prediction never reads through; no step counter is touched
+  const ManageArgs a = make_args(pred_ids, mk, E, S, E, max_inserts, table, map_cold,
+                                 slot_expert, slot_stamp, routed, nullptr, miss, n_miss, 0, 0,
+                                 nullptr);
+  return launch_prefetch(a, stream);
 }
 
 int expert_cache_remap(const void* ids, int n, int id_bytes, const int* table, int E,

@@ -115,9 +115,16 @@ constexpr int table_chunks(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256
 
 // One policy step. On return, the updated table is in L.tab (or in memory for GLOBAL_E)
 // and idv holds ids[lane + 64k] (or -1 past mk). TQ table chunks are held in registers.
-template <int CS, bool GLOBAL_E, int IDB, int TQ>
+//
+// PF makes it the prefetch step for predicted ids: the step counter is neither read nor
+// written, resident predicted experts keep their stamps, there is no ageing, and installs
+// get stamp 0 -- below any stamp a real step gives, so an unused prediction is the first
+// victim later and a used one gets, at its first real hit, the stamp a real install would
+// have given it (st under LRU, 1 under LFU). Victims are chosen exactly as in a real step.
+template <int CS, bool GLOBAL_E, int IDB, int TQ, bool PF = false>
 __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBAL_E>& L,
                                             long long (&idv)[kIdRegs]) {
+  static_assert(!PF || IDB == 4, "prefetch takes int32 ids");
   const int lane = __lane_id();
   const int E = a.E, S = a.S, mk = a.mk;
 
@@ -126,12 +133,16 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   // branch; lanes past the end substitute their sentinel after the loads return. The step
   // counter is a vector load: a scalar load would count in lgkmcnt, and every LDS fence
   // below would stall on it.
-  const long long st_v = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  long long st_v = 0;
+  if constexpr (!PF)
+    st_v = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // No branch around the id loads either (a branch join would make the compiler wait for
-  // them before issuing the rest): with no ids, they read the 8-byte step counter instead.
+  // them before issuing the rest): with no ids, they read the 8-byte step counter (the
+  // prefetch step: the first table entry) instead.
   using IdT = typename std::conditional<IDB == 8, long long, int>::type;
-  const IdT* ip = mk > 0 ? reinterpret_cast<const IdT*>(a.ids)
-                         : reinterpret_cast<const IdT*>(a.step);
+  const IdT* dummy = PF ? reinterpret_cast<const IdT*>(a.table)
+                        : reinterpret_cast<const IdT*>(a.step);
+  const IdT* ip = mk > 0 ? reinterpret_cast<const IdT*>(a.ids) : dummy;
   const int last_id = mk > 0 ? mk - 1 : 0;
   IdT raw[kIdRegs];
 #pragma unroll
@@ -225,7 +236,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     }
     if (cnt > a.max_distinct) {  // wide step: read through, nothing else changes
       if (lane == 0) {
-        a.step[0] = st_v + 1;
+        if constexpr (!PF) a.step[0] = st_v + 1;
         a.n_miss[0] = 0;
       }
       return;
@@ -235,7 +246,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
       if (u < nchunk) {
         const int e = lane + u * kWave;
         const int t = tv[u];
-        if (fl[u] && t >= 0 && t < S) L.hit[t] = 1;
+        if (!PF && fl[u] && t >= 0 && t < S) L.hit[t] = 1;
         const bool m = fl[u] && t < 0;
         const unsigned long long mask = __ballot(m);
         const int j = total + __popcll(mask & lanes_below());
@@ -254,7 +265,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     }
     if (cnt > a.max_distinct) {
       if (lane == 0) {
-        a.step[0] = st_v + 1;
+        if constexpr (!PF) a.step[0] = st_v + 1;
         a.n_miss[0] = 0;
       }
       return;
@@ -269,7 +280,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
         else
           t = L.tab[e];
       }
-      if (f && t >= 0 && t < S) L.hit[t] = 1;
+      if (!PF && f && t >= 0 && t < S) L.hit[t] = 1;
       const bool m = f && t < 0;
       const unsigned long long mask = __ballot(m);
       const int j = total + __popcll(mask & lanes_below());
@@ -296,21 +307,21 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
     const int x = se[c];
-    const bool hit = (s < S) & (hv[c] != 0);
+    const bool hit = !PF && (s < S) & (hv[c] != 0);
     fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
     if (hit) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
     if (nins == 0 && hit) a.slot_stamp[s] = sp[c];
   }
   if (nins == 0) {  // no inserts: refreshed stamps only, no ageing
     if (lane == 0) {
-      a.step[0] = st;
+      if constexpr (!PF) a.step[0] = st;
       a.n_miss[0] = 0;
     }
     return;
   }
 
   // LFU ageing on inserting steps where st % decay == 0
-  if (!lru && a.decay > 0 && (st % (long long)a.decay) == 0) {
+  if (!PF && !lru && a.decay > 0 && (st % (long long)a.decay) == 0) {
 #pragma unroll
     for (int c = 0; c < CS; ++c) sp[c] >>= 1;
   }
@@ -327,7 +338,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     nev += __popcll(__ballot(ev[c]));
   }
   const int nact = min(nins, nev);
-  const long long fresh = lru ? st : 1;
+  const long long fresh = PF ? 0 : lru ? st : 1;
 
   if (use_argmin<CS>(nact, nev)) {
     // ---- few inserts: repeated wave-min, each insert installed as soon as it is found.
@@ -504,7 +515,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     }
   }
   if (lane == 0) {
-    a.step[0] = st;
+    if constexpr (!PF) a.step[0] = st;
     a.n_miss[0] = nact;
   }
 }
@@ -552,6 +563,15 @@ __global__ __launch_bounds__(kWave) void manage_k(ManageArgs a) {
     else lds_sync();
     remap_tail<GLOBAL_E, IDB>(a, L, idv);
   }
+}
+
+// The prefetch step (manage_step with PF) for int32 predicted ids.
+template <int CS, bool GLOBAL_E, int TQ>
+__global__ __launch_bounds__(kWave) void prefetch_k(ManageArgs a) {
+  __shared__ ManageLds<GLOBAL_E> L;
+  args_in_sgprs(a);
+  long long idv[kIdRegs];
+  manage_step<CS, GLOBAL_E, 4, TQ, true>(a, L, idv);
 }
 
 // Standalone remap, any grid; one id per lane per iteration.

@@ -1,10 +1,11 @@
 """ctypes binding of libexpertcache.so (C-ABI in include/expert_cache.h).
 
 Same search order and same argument lists for the reference's two bound entry points
-(vllm_expert_cache/_lib.py:15-61): manage and gather. Three more are bound here:
-`expert_cache_fused` (exported by the reference but never bound), and the two remap entry
-points that replace the reference's torch remap. Every call is asynchronous on the caller's
-stream and never reads a device value back, so the whole path is HIP-graph capturable.
+(vllm_expert_cache/_lib.py:15-61): manage and gather. Four more are bound here:
+`expert_cache_fused` (exported by the reference but never bound), the two remap entry
+points that replace the reference's torch remap, and `expert_cache_prefetch`. Every call is
+asynchronous on the caller's stream and never reads a device value back, so the whole path
+is HIP-graph capturable.
 
 There is no fallback: if the library or one of its symbols is missing, loading fails with
 an error that says so.
@@ -41,6 +42,9 @@ SIGNATURES = {
     #              slot_expert, slot_stamp, routed, step, miss, n_miss, policy, decay, out,
     #              stream)
     "expert_cache_manage_remap": [_P] + [_I] * 6 + [_P] * 8 + [_I] * 2 + [_P, _P],
+    # prefetch(pred_ids, mk, E, S, max_inserts, table, map_cold, slot_expert, slot_stamp,
+    #          routed, miss, n_miss, stream)
+    "expert_cache_prefetch": [_P] + [_I] * 4 + [_P] * 7 + [_P],
 }
 
 

@@ -193,7 +193,9 @@ def arm(layer, method, logger) -> bool:
     def apply(layer, x, topk_weights, topk_ids, shared_experts=None,
               shared_experts_input=None):
         if not cache.fits(topk_ids):
-            # wide (prefill) step: read through the host copies on the stock path
+            # wide (prefill) step: read through the host copies on the stock path; a
+            # prefetch still copying is joined so no side-stream work is left behind
+            cache.join()
             return orig_apply(layer, x, topk_weights, topk_ids, shared_experts,
                               shared_experts_input)
         slot_ids = cache.refresh(topk_ids)

@@ -15,6 +15,12 @@ reads a device value back to the host, so the sequence is graph-capturable, and 
 are deterministic, so tensor-parallel ranks seeing the same routing keep identical caches
 without talking to each other.
 
+A caller that can predict a layer's next routing (for instance from the previous layer's
+hidden state) calls `prefetch` early: the install-only policy step runs on the current
+stream and the copy of the predicted experts on a side stream, overlapping what follows;
+the layer's next `refresh` waits for that copy before its own gather. README.md:392-394 of
+the reference names this as the path's next step.
+
 Constructor, attributes and methods mirror vllm_expert_cache/cache.py:38-163 of the
 reference (`fits`, `remap`, `refresh`, `slots`, `bound`, `names`, `skipped`, `E`, `S`).
 """
@@ -35,6 +41,16 @@ from .config import settings
 # 4.7 MB expert, 512 reach ~41 GB/s), hence 32 x 1 rather than the reference's 16 x 64.
 DEFAULT_CHUNKS = 32
 DEFAULT_LANES = 1
+
+# One side stream per device carries every layer's prefetch copy: the copies share one host
+# link, so running them one after another loses nothing. Default priority.
+_SIDE: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    if device not in _SIDE:
+        _SIDE[device] = torch.cuda.Stream(device)
+    return _SIDE[device]
 
 
 def _bytes_per_expert(t: torch.Tensor) -> int:
@@ -113,6 +129,12 @@ class ExpertSlotCache:
         self.step = torch.zeros((1,), dtype=i64, device=device)
         self.miss = torch.zeros((2 * self.S,), dtype=i32, device=device)
         self.n_miss = torch.zeros((1,), dtype=i32, device=device)
+        # the prefetch step's own miss list: its copy may still read it while the next real
+        # step writes `miss`
+        self.pf_miss = torch.zeros((2 * self.S,), dtype=i32, device=device)
+        self.pf_n_miss = torch.zeros((1,), dtype=i32, device=device)
+        self._pf_done = None
+        self._pf_pending = False
 
         self.policy = settings.policy_code
         self.decay = settings.decay
@@ -161,7 +183,54 @@ class ExpertSlotCache:
             _ptr(self.n_miss), self.policy, self.decay, _ptr(out), stream)
         if rc != 0:
             raise RuntimeError(f"expert_cache_manage failed rc={rc}")
+        # a prefetched slot may be this step's victim: its copy lands before this gather
+        self.join()
+        self._gather(self.miss, self.n_miss, stream)
+        return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
 
+    def prefetch(self, pred_ids: torch.Tensor, max_inserts: int | None = None) -> bool:
+        """Start bringing the experts predicted for this layer's next step into slots.
+
+        The prefetch policy step (expert_cache_prefetch: installs at stamp 0, no step
+        advance, resident predictions untouched, at most `max_inserts` installs, at most and
+        by default S)
+        runs on the current stream; the copy of what it installed runs on the device's side
+        stream, so it overlaps whatever the current stream does next. This layer's next
+        `refresh`, or `join`, makes the current stream wait for the copy. Returns False, and
+        does nothing, when the prediction has more ids than there are slots."""
+        ids = pred_ids if pred_ids.dtype == torch.int32 else pred_ids.to(torch.int32)
+        ids = ids.contiguous()
+        mk = int(ids.numel())
+        if mk > self.S:
+            return False
+        self.join()  # the previous copy may still read pf_miss
+        cur = torch.cuda.current_stream(self.table.device)
+        rc = lib().expert_cache_prefetch(
+            _ptr(ids), mk, self.E, self.S,
+            self.S if max_inserts is None else min(int(max_inserts), self.S),
+            _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
+            _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.pf_miss),
+            _ptr(self.pf_n_miss), ctypes.c_void_p(cur.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"expert_cache_prefetch failed rc={rc}")
+        side = _side_stream(self.table.device)
+        side.wait_stream(cur)
+        self._gather(self.pf_miss, self.pf_n_miss, ctypes.c_void_p(side.cuda_stream))
+        if self._pf_done is None:
+            self._pf_done = torch.cuda.Event()
+        self._pf_done.record(side)
+        self._pf_pending = True
+        return True
+
+    def join(self) -> None:
+        """Make the current stream wait for this layer's pending prefetch copy, if any."""
+        if self._pf_pending:
+            torch.cuda.current_stream(self.table.device).wait_event(self._pf_done)
+            self._pf_pending = False
+
+    def _gather(self, miss: torch.Tensor, n_miss: torch.Tensor, stream) -> None:
+        """expert_cache_gather of every mirrored tensor over one miss list, six per call."""
+        h = lib()
         dsts = [self.slots[n] for n in self.names]
         srcs = [getattr(self.owner, n).data for n in self.names]
         for i in range(0, len(dsts), GATHER_SLOTS):
@@ -173,9 +242,7 @@ class ExpertSlotCache:
             for d, s in zip(gd, gs):
                 args += [_ptr(d), ctypes.c_void_p(device_address(s)),
                          ctypes.c_long(_bytes_per_expert(s))]
-            rc = h.expert_cache_gather(*args, _ptr(self.miss), _ptr(self.n_miss),
-                                       self.chunks, self.lanes, stream)
+            rc = h.expert_cache_gather(*args, _ptr(miss), _ptr(n_miss), self.chunks,
+                                       self.lanes, stream)
             if rc != 0:
                 raise RuntimeError(f"expert_cache_gather failed rc={rc}")
-
-        return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
