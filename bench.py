@@ -21,6 +21,11 @@ Printed (one JSON line on stdout):
   cpu_baseline the CPU path on this box's host: the policy restated in C (oracle/) on one
                core deciding the misses, and one hipMemcpyAsync per (miss, buffer), on a
                sample of the same steps
+  prefetch     a window of the timed steps with and without next-layer prefetch (each
+               layer's predicted experts installed by expert_cache_prefetch and copied on a
+               side stream during the previous layer), with no model compute and with a
+               50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
+               routing: an upper bound) and 0.8 (each id wrong with probability 0.2)
 
     python bench.py [--steps K] [--warmup W] [--slots 64] [--policy lfu]
 """
@@ -72,6 +77,8 @@ def parse():
                    help="timed steps in the CPU-baseline sample (0 to skip)")
     p.add_argument("--chunks", type=int, default=None)
     p.add_argument("--lanes", type=int, default=None)
+    p.add_argument("--no-prefetch", action="store_true",
+                   help="skip the next-layer prefetch leg")
     p.add_argument("--traffic-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: 16 gathers of one expert each and 8 plain "
                         "device copies of 64 MiB (the counter calibration), nothing else")
@@ -398,6 +405,11 @@ def main():
         cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
                            policy, decay, W, dev)
 
+    prefetch = None
+    if not args.no_prefetch:
+        prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[W], L, E, S,
+                                mk, policy, decay, W, T, B_exp, chunks, lanes, dev, peak)
+
     sweep = None
     if not args.no_hit_sweep:
         sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
@@ -447,6 +459,7 @@ def main():
                      "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
                                  "kernel on one 256 MB slab)"},
         "cpu_baseline": cpu,
+        "prefetch": prefetch,
         "hit_rate_sweep": sweep,
     }
     print(json.dumps(res), flush=True)
@@ -514,6 +527,149 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
 
 def _row(t, l):
     return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
+
+
+def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
+                 W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
+                 accuracies=(None, 1.0, 0.8)):
+    """Next-layer prefetch over a window of the timed steps, every run from the same start
+    state, as one captured graph per decode step:
+      without prefetch: per layer l, manage+remap(l), gather(l), compute(l);
+      with prefetch:    layer 0's prefetch first, then per layer l the prefetch of layer
+                        l+1 (policy step on the launch stream, copy on a side stream),
+                        manage+remap(l), a wait for layer l's prefetch copy, gather(l) of
+                        what is still missing, compute(l).
+    compute(l) stands in for the layer's attention and expert GEMMs: a spin of C us on one
+    CU (C = 0: no compute, so prefetch has nothing to hide behind). The predictor is the true
+    routing with each id replaced, with probability 1 - accuracy, by a random expert;
+    accuracy 1.0 is an upper bound no real predictor reaches."""
+    K = min(window, T - W)
+    i32 = torch.int32
+    tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
+    routed = np.zeros((K, L, E), bool)
+    for i in range(mk):
+        routed[tt, ll, ids_np[W:W + K, :, i]] = True
+    distinct = int(routed.sum())
+
+    # spin cycles per microsecond, measured
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    torch.cuda._sleep(int(2e6))
+    b.record()
+    torch.cuda.synchronize()
+    cyc_per_us = 2e6 / (a.elapsed_time(b) * 1e3)
+
+    st = Layers(torch, L, E, S, dev)
+    pf_miss = torch.zeros((L, 2 * S), dtype=i32, device=dev)
+    pf_nm = torch.zeros((L,), dtype=i32, device=dev)
+    ids_static = torch.zeros((L, mk), dtype=i32, device=dev)
+    pred_static = torch.zeros((L, mk), dtype=i32, device=dev)
+    out_static = torch.zeros((L, mk), dtype=i32, device=dev)
+    nm_static = torch.zeros((L,), dtype=i32, device=dev)
+    nm_hist = torch.zeros((K, L), dtype=i32, device=dev)
+    pf_hist = torch.zeros((K, L), dtype=i32, device=dev)
+    pf_miss_hist = torch.zeros((K, L, 2 * S), dtype=i32, device=dev)
+    side = torch.cuda.Stream(dev)
+    done = [torch.cuda.Event() for _ in range(L)]
+    m_args = [(_row(ids_static, l), 4, mk, E, S, min(E, mk), S, st.row("table", l),
+               st.row("map_cold", l), st.row("slot_expert", l), st.row("slot_stamp", l),
+               st.row("routed", l), st.row("step", l), st.row("miss", l),
+               _row(nm_static, l), policy, decay, _row(out_static, l)) for l in range(L)]
+    p_args = [(_row(pred_static, l), mk, E, S, S, st.row("table", l), st.row("map_cold", l),
+               st.row("slot_expert", l), st.row("slot_stamp", l), st.row("routed", l),
+               _row(pf_miss, l), _row(pf_nm, l)) for l in range(L)]
+    gp_args = [tuple(g_args[l][:18]) + (_row(pf_miss, l), _row(pf_nm, l), chunks, lanes)
+               for l in range(L)]
+    gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
+               for l in range(L)]
+
+    def launch(cur, prefetch, spin):
+        c = ctypes.c_void_p(cur.cuda_stream)
+        sd = ctypes.c_void_p(side.cuda_stream)
+
+        def pf(l):
+            rc = lib.expert_cache_prefetch(*p_args[l], c)
+            side.wait_stream(cur)
+            rc |= lib.expert_cache_gather(*gp_args[l], sd)
+            done[l].record(side)
+            return rc
+
+        rc = pf(0) if prefetch else 0
+        for l in range(L):
+            if prefetch and l + 1 < L:
+                rc |= pf(l + 1)
+            rc |= lib.expert_cache_manage_remap(*m_args[l], c)
+            if prefetch:
+                cur.wait_event(done[l])
+            rc |= lib.expert_cache_gather(*gr_args[l], c)
+            if spin:
+                torch.cuda._sleep(spin)
+        if rc:
+            raise RuntimeError(f"decode step launch failed rc={rc}")
+
+    out = []
+    base_ms = {}
+    for C in compute:
+        for q in accuracies:
+            if q is None:
+                pred = None
+            else:
+                rng = np.random.default_rng(int(q * 1000))
+                pred = ids_np[W:W + K].copy()
+                if q < 1.0:
+                    wrong = rng.random(pred.shape) >= q
+                    pred[wrong] = rng.integers(0, E, int(wrong.sum()))
+                pred_dev = torch.as_tensor(pred, device=dev)
+            st.restore(snap)
+            pf_nm.zero_()
+            pf_hist.zero_()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                launch(torch.cuda.current_stream(), q is not None, int(C * cyc_per_us))
+            torch.cuda.synchronize()
+            wall0 = time.perf_counter()
+            a.record()
+            for t in range(K):
+                ids_static.copy_(ids_dev[W + t], non_blocking=True)
+                if pred is not None:
+                    pred_static.copy_(pred_dev[t], non_blocking=True)
+                g.replay()
+                nm_hist[t].copy_(nm_static, non_blocking=True)
+                if pred is not None:
+                    pf_hist[t].copy_(pf_nm, non_blocking=True)
+                    pf_miss_hist[t].copy_(pf_miss, non_blocking=True)
+            b.record()
+            torch.cuda.synchronize()
+            elapsed = max(time.perf_counter() - wall0, a.elapsed_time(b) * 1e-3)
+            del g
+            nm, pn = nm_hist.cpu().numpy(), pf_hist.cpu().numpy()
+            used = 0
+            if pred is not None:
+                fetched = pf_miss_hist.cpu().numpy()[..., 0::2]
+                valid = np.arange(S)[None, None, :] < pn[..., None]
+                used = int((routed[tt[..., None], ll[..., None], np.where(valid, fetched, 0)]
+                            & valid).sum())
+            moved = int(nm.sum() + pn.sum())
+            ms = 1e3 * elapsed / K
+            if q is None:
+                base_ms[C] = ms
+            gbps = moved * B_exp / elapsed / 1e9
+            out.append({"compute_us_per_layer": C, "predictor_accuracy": q,
+                        "ms_per_step": round(ms, 4),
+                        "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
+                        "moved_GBps": round(gbps, 3),
+                        "moved_frac_of_link_peak": round(gbps / peak, 4),
+                        "prefetch_inserts": int(pn.sum()), "prefetch_used": used,
+                        "critical_path_inserts": int(nm.sum()),
+                        "real_step_hit_rate": round(1.0 - float(nm.sum()) / distinct, 5)})
+            log(f"prefetch leg, compute {C} us/layer, predictor "
+                f"{'none' if q is None else q}: {ms:.3f} ms/step "
+                f"({base_ms[C] / ms:.3f}x), {moved} experts moved at {gbps:.2f} GB/s, "
+                f"{int(pn.sum())} prefetched ({used} used), {int(nm.sum())} on the critical "
+                f"path")
+    return {"window_steps": K, "timed_trace_steps": [W, W + K],
+            "spin_cycles_per_us": round(cyc_per_us, 1), "runs": out}
 
 
 def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
