@@ -252,3 +252,69 @@ def test_cache_prefetch_under_graph_capture():
         for n in NAMES:
             assert torch.equal(graphed.slots[n], eager.slots[n]), (t, n)
         _all_slots_hold_their_experts(graphed, src)
+
+
+def test_cache_prefetch_edge_cases(monkeypatch):
+    """Two prefetches in a row (the second waits for the first copy), a budget of one
+    install, an over-long prediction (refused, nothing launched), and join() with nothing
+    pending."""
+    monkeypatch.setenv("EXPERT_CACHE_POLICY", "lfu")
+    monkeypatch.setenv("EXPERT_CACHE_DECAY", "64")
+    owner = Owner(4)
+    src = _device_sources(owner)
+    cache = ExpertSlotCache(owner, NAMES, E, S, gu.DEV)
+    ref = oracle.State(E, S)
+    cache.join()
+    rng = np.random.default_rng(31)
+    for t in range(30):
+        ids = rng.choice(E, K, replace=False).astype(np.int32)
+        p1 = rng.choice(E, K, replace=False).astype(np.int32)
+        p2 = _predict(ids, E, 0.5, rng).astype(np.int32)
+        assert cache.prefetch(torch.as_tensor(p1, device=gu.DEV))
+        assert cache.prefetch(torch.as_tensor(p2, device=gu.DEV), max_inserts=1)
+        assert not cache.prefetch(torch.zeros(S + 1, dtype=torch.int32, device=gu.DEV))
+        slot_ids = cache.refresh(torch.as_tensor(ids, device=gu.DEV))
+        assert ref.prefetch(p1, S) == 0
+        assert ref.prefetch(p2, 1) == 0
+        assert ref.n_miss[0] <= 1
+        assert ref.manage(ids, K, S, 1, 64) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(slot_ids.cpu().numpy(), oracle.remap(ids, ref.table)), t
+        for f in ("table", "slot_expert", "slot_stamp", "step"):
+            assert np.array_equal(getattr(cache, f).cpu().numpy(), getattr(ref, f)), (t, f)
+        _all_slots_hold_their_experts(cache, src)
+
+
+def test_two_layer_pipeline_shares_the_side_stream():
+    """The plugin's order over two layers: layer 1's prefetch is issued while layer 0
+    refreshes, through the one side stream; every resident slot of both layers holds its
+    expert's bytes after each step."""
+    owners = [Owner(5), Owner(6)]
+    srcs = [_device_sources(o) for o in owners]
+    caches = [ExpertSlotCache(o, NAMES, E, S, gu.DEV) for o in owners]
+    rng = np.random.default_rng(41)
+    busy = torch.randn((1024, 1024), device=gu.DEV)
+    nxt0 = rng.choice(E, K, replace=False).astype(np.int32)
+    for t in range(40):
+        ids0 = nxt0
+        ids1 = rng.choice(E, K, replace=False).astype(np.int32)
+        nxt0 = rng.choice(E, K, replace=False).astype(np.int32)
+        assert caches[1].prefetch(torch.as_tensor(_predict(ids1, E, 0.75, rng), device=gu.DEV))
+        s0 = caches[0].refresh(torch.as_tensor(ids0, device=gu.DEV))
+        t0 = caches[0].table.clone()  # the table the step's slot ids refer to
+        busy = busy @ busy.T * 1e-3
+        s1 = caches[1].refresh(torch.as_tensor(ids1, device=gu.DEV))
+        t1 = caches[1].table.clone()
+        # the next step's prefetch for layer 0 may evict this step's experts: it is ordered
+        # after everything already queued on the stream
+        assert caches[0].prefetch(torch.as_tensor(nxt0, device=gu.DEV))
+        torch.cuda.synchronize()
+        for c, src in zip(caches, srcs):
+            _all_slots_hold_their_experts(c, src)
+        for table, ids, out in ((t0, ids0, s0), (t1, ids1, s1)):
+            table = table.cpu().numpy()
+            assert np.array_equal(out.cpu().numpy(), table[ids]), t
+            assert (table[ids] >= 0).all()
+    caches[0].join()
+    torch.cuda.synchronize()
+    _all_slots_hold_their_experts(caches[0], srcs[0])
