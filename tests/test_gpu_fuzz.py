@@ -5,7 +5,8 @@ S up to 1024), mk (including 0 and more than 256 ids), ids with padding and out-
 values, max_distinct (including below the routed count: read-through), max_inserts
 (including 0 and caps below the miss count), policy and decay, and a random consistent warm
 state with random stamps. Each step is compared on every field, and the fused remap output
-against the closed form.
+against the closed form. The prefetch step runs over the same space, interleaved with
+manage steps.
 """
 from __future__ import annotations
 
@@ -110,3 +111,54 @@ def test_extreme_stamps(seed):
                           ("step", st.step[0]), ("miss", st.miss[0]), ("n_miss", st.n_miss[0])):
             got, want = dev.cpu().numpy(), getattr(ref, name)
             assert np.array_equal(got, want), f"{tag}: {name} differs at {gu.first_diff(got, want)}"
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_prefetch(seed):
+    """The prefetch step over the same random shapes and warm states: each step runs a
+    prefetch of random ids (padding and out-of-range included, any budget) into a miss
+    list of its own, then a manage step, and both are compared on every field."""
+    rng, E, S, mk, mi, policy, decay, hot, slots, stamps = _case(5000 + seed)
+    pcap = max(S, 1024)
+    st, ref = _device_state(E, S, mi, hot, slots, stamps)
+    pf_miss = torch.zeros((2 * pcap,), dtype=torch.int32, device=gu.DEV)
+    pf_n = torch.zeros((1,), dtype=torch.int32, device=gu.DEV)
+    ref_pf, ref_pn = np.zeros(2 * pcap, np.int32), np.zeros(1, np.int32)
+    ref_big = oracle.State(E, S, miss_cap=pcap)  # carries the prefetch's miss list
+    for t in range(STEPS):
+        pk = int(rng.choice([0, 1, 8, mk, 300]))
+        budget = int(rng.choice([0, 1, 4, S, 1024]))
+        pred = rng.integers(-3, E + 3, size=pk).astype(np.int32)
+        d_pred = torch.as_tensor(pred, device=gu.DEV)
+        rc = gu.lib().expert_cache_prefetch(
+            gu.ptr(d_pred) if pk else None, pk, E, S, budget, st.row("table", 0),
+            st.row("map_cold", 0), st.row("slot_expert", 0), st.row("slot_stamp", 0),
+            st.row("routed", 0), gu.ptr(pf_miss), gu.ptr(pf_n), gu.stream())
+        assert rc == 0
+        for f in ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "step"):
+            setattr(ref_big, f, getattr(ref, f))  # shared arrays: one state, two miss lists
+        ref_big.miss[:], ref_big.n_miss[:] = ref_pf, ref_pn
+        assert ref_big.prefetch(pred, budget) == 0
+        ref_pf, ref_pn = ref_big.miss.copy(), ref_big.n_miss.copy()
+        torch.cuda.synchronize()
+        tag = f"seed {seed} step {t}: E={E} S={S} pk={pk} budget={budget}"
+        for name, dev, want in (("table", st.table[0], ref.table),
+                                ("map_cold", st.map_cold[0], ref.map_cold),
+                                ("slot_expert", st.slot_expert[0], ref.slot_expert),
+                                ("slot_stamp", st.slot_stamp[0], ref.slot_stamp),
+                                ("routed", st.routed[0], ref.routed), ("step", st.step[0], ref.step),
+                                ("pf_miss", pf_miss, ref_pf), ("pf_n", pf_n, ref_pn)):
+            got = dev.cpu().numpy()
+            assert np.array_equal(got, want), f"{tag}: {name} differs at {gu.first_diff(got, want)}"
+        ids = rng.integers(-3, E + 3, size=mk).astype(np.int32)
+        d_ids = torch.as_tensor(ids, device=gu.DEV)
+        md = min(E, mk)
+        assert gu.manage_call(gu.lib(), st, 0, gu.ptr(d_ids) if mk else None, mk, md, mi,
+                              policy, decay) == 0
+        assert ref.manage(ids, md, mi, policy, decay) == 0
+        torch.cuda.synchronize()
+        for name, dev in (("table", st.table[0]), ("slot_expert", st.slot_expert[0]),
+                          ("slot_stamp", st.slot_stamp[0]), ("step", st.step[0]),
+                          ("miss", st.miss[0]), ("n_miss", st.n_miss[0])):
+            got, want = dev.cpu().numpy(), getattr(ref, name)
+            assert np.array_equal(got, want), f"{tag} (manage): {name} differs at {gu.first_diff(got, want)}"
