@@ -399,6 +399,22 @@ def main():
     log(f"link peak: hipMemcpyAsync H2D {memcpy_gbps:.2f} GB/s, gather kernel on one 256 MB "
         f"slab {kernel_gbps:.2f} GB/s")
 
+    # ---- latency floor: an empty kernel node in a graph (48 per replay) --------------------
+    ge = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ge):
+        for _ in range(L):
+            torch.cuda._sleep(0)
+    ge.replay()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(200):
+        ge.replay()
+    b.record()
+    torch.cuda.synchronize()
+    empty_us = a.elapsed_time(b) * 1e3 / (200 * L)
+    del ge
+    log(f"empty kernel node in a graph: {empty_us:.2f} us")
+
     # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer) --------------
     cpu = None
     if args.cpu_steps > 0:
@@ -445,6 +461,7 @@ def main():
         "manage_remap_us_per_layer": manage_us,
         "manage_remap_def": manage_def,
         "manage_remap_us_per_layer_events": round(float(man_us.mean()), 3),
+        "empty_kernel_graph_us": round(empty_us, 3),
         "manage_remap_counters": _manage_counters(),
         "gather_us_per_launch": round(float(gat_us.mean()), 3),
         "gather_GBps_launches_with_miss": None if per_miss is None else round(per_miss, 3),
@@ -491,6 +508,18 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         oracle.run_trace(np.ascontiguousarray(ids_np[W:W + n, l]), E, S, policy, decay,
                          state=pol_states[l])
     policy_us = (oracle.now() - t0) / (n * L) * 1e6
+    # the same policy work spread over host threads, one layer at a time per thread (the C
+    # call releases the interpreter lock); layers are independent
+    from concurrent.futures import ThreadPoolExecutor
+    threads = max(1, min(16, os.cpu_count() or 1, L))
+    par_states = [s.copy() for s in states]
+    t0 = oracle.now()
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda l: oracle.run_trace(np.ascontiguousarray(ids_np[W:W + n, l]), E, S,
+                                               policy, decay, state=par_states[l]), range(L)))
+    policy_par_us = (oracle.now() - t0) / (n * L) * 1e6
+    for a_, b_ in zip(pol_states, par_states):
+        assert np.array_equal(a_.table, b_.table), "threaded policy diverged"
     torch.cuda.synchronize()
     moved = 0
     t0 = time.perf_counter()
@@ -514,13 +543,16 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         hbuf.copy_(hsrc)
     host_memcpy = 4 * (256 << 20) / (time.perf_counter() - t1) / 1e9
     log(f"cpu baseline: {n} steps x {L} layers, {moved / 1e9:.2f} GB in {wall:.2f}s -> "
-        f"{moved / wall / 1e9:.2f} GB/s; policy {policy_us:.3f} us/layer-step; host memcpy "
+        f"{moved / wall / 1e9:.2f} GB/s; policy {policy_us:.3f} us/layer-step (one core), "
+        f"{policy_par_us:.3f} us/layer-step over {threads} threads; host memcpy "
         f"{host_memcpy:.1f} GB/s")
     return {"value": round(moved / wall / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"timed steps {W}..{W + n} of the trace x {L} layers from the same start "
                       f"state: C policy (oracle/policy.c) per layer-step, then one "
                       f"hipMemcpyAsync H2D per (miss, buffer)",
             "policy_us_per_layer_step": round(policy_us, 4),
+            "policy_us_per_layer_step_threads": round(policy_par_us, 4),
+            "policy_threads": threads,
             "host_memcpy_GBps": round(host_memcpy, 2),
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
 
