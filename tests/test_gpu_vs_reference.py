@@ -8,11 +8,12 @@ captured in HIP graphs so that host launch cost is out of the picture:
   * the reference's timing shapes (tests/test_policy.py:283-318): E=512, S=257, 50 routing
     ids per step, LRU, six buffers of 1,308,800 B per expert; manage at steady state and
     gather of 1, 2, 8, 52 and 64 experts;
-  * a decode loop of the 48-layer-e128 workload (8 of its layers, 64 slots, LFU, cold start)
-    through each side's per-layer refresh: the reference's as cache.py:112-163 does it
-    (manage, gather on its 16 x 64 default grid, torch remap), this library's as
-    vllm_expert_cache/cache.py does it (manage with the fused remap, gather on its default
-    grid).
+  * a decode loop (LFU, cold start) through each side's per-layer refresh: the reference's
+    as cache.py:112-163 does it (manage, gather on its 16 x 64 default grid, torch remap),
+    this library's as vllm_expert_cache/cache.py does it (manage with the fused remap,
+    gather on its default grid). Four workloads: 48-layer-e128 (8 of its layers, 64 slots),
+    its batch-4 form (48 slots), 352 MB bf16 experts (4 slots) and 44 MB fp8 experts
+    (4 layers, 128 slots, 128 ids per step).
 
 Each test prints one "speed:" line per figure (run pytest with -s to see them) and asserts
 this library is not slower than the reference beyond a 5 % noise margin. EC_SPEED_ASSERT=0
@@ -176,10 +177,14 @@ def test_gather_vs_reference(store_512, n):
 
 # ---- the 48-layer-e128 decode loop through each side's refresh -----------------------------
 
-def test_decode_loop_vs_reference():
+@pytest.mark.parametrize("name,S,L,T", [("48-layer-e128", 64, 8, 512),
+                                         ("48-layer-e128-batch4", 48, 8, 512),
+                                         ("8-layer-e8-bf16", 4, 8, 96),
+                                         ("8-layer-e256-fp8", 128, 4, 48)])
+def test_decode_loop_vs_reference(name, S, L, T):
     ref = _ref()
-    w = traces.WORKLOADS["48-layer-e128"]
-    L, T, S, E, mk = 8, 512, 64, w.experts, w.mk
+    w = traces.WORKLOADS[name]
+    E, mk = w.experts, w.mk
     bufs = [b.nbytes for b in w.buffers]
     B_exp = sum(bufs)
     ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)
@@ -194,6 +199,7 @@ def test_decode_loop_vs_reference():
         return P(t.data_ptr() + l * t.stride(0) * t.element_size())
 
     runs = {}
+    workload = name
     for name in ("reference", "this"):
         h = ref if name == "reference" else gu.lib()
         st = gu.Layers(L, E, S)
@@ -279,7 +285,7 @@ def test_decode_loop_vs_reference():
     inserts = int(m["nm"].sum())
     assert inserts > 0
     gb = inserts * B_exp / 1e9
-    _say(f"decode loop 48-layer-e128 ({L} layers x {T} steps, S={S}, LFU, {inserts} inserts, "
+    _say(f"decode loop {workload} ({L} layers x {T} steps, S={S}, LFU, {inserts} inserts, "
          f"{gb:.1f} GB): reference {r['ms']:.1f} ms ({gb / r['ms'] * 1e3:.1f} GB/s), "
          f"this {m['ms']:.1f} ms ({gb / m['ms'] * 1e3:.1f} GB/s)")
     assert _not_slower(m["ms"], r["ms"])
