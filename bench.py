@@ -437,6 +437,7 @@ def main():
             manage_def = ("in-graph cost per layer of the policy+remap kernel alone over the "
                           "whole trace at this budget and policy (hit-rate pass)")
 
+    traffic = _traffic()
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -469,7 +470,8 @@ def main():
                            "gather_kernel_256MB": round(kernel_gbps, 3)},
         "roofline": {"bound": "host-link", "kernel": "gather_k", "achieved": round(achieved, 3),
                      "peak": round(peak, 3), "unit": "GB/s", "frac": round(achieved / peak, 4),
-                     "traffic": _traffic(),
+                     "traffic": None if traffic is None else traffic["bytes_per_launch"],
+                     "traffic_detail": traffic,
                      "achieved_def": f"gathered bytes / summed gather kernel time, {nseg} "
                                      f"segments x {seg_len} of the timed steps x {L} layers, "
                                      f"HIP events around each launch",
@@ -781,9 +783,12 @@ def _traffic():
         t = json.loads(p.read_text())
     except (OSError, ValueError):
         return None
-    return {"fetch_bytes_per_miss": t["fetch_bytes_per_launch"],
+    return {"bytes_per_launch": t["fetch_bytes_per_launch"] + t["write_bytes_per_launch"],
+            "launch": "one expert (4,732,928 B) per launch",
+            "fetch_bytes_per_miss": t["fetch_bytes_per_launch"],
             "write_bytes_per_miss": t["write_bytes_per_launch"],
             "algorithmic_bytes_per_miss": t["algorithmic_bytes_per_launch"],
+            "algorithmic_read_plus_write": 2 * t["algorithmic_bytes_per_launch"],
             "fetch_over_algorithmic": t["fetch_over_algorithmic"],
             "source": f"profiles/{p.name}"}
 
