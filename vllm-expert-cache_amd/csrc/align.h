@@ -35,8 +35,6 @@ constexpr int kStage = 10240;
 struct AlignLds {
   int cur_h[kMaxSlots + 1];          // counts, then placement cursors, per slot bucket
   int cur_c[kMaxAlignExperts + 1];   // same per expert bucket
-  int cum_h[kMaxSlots + 1];
-  int cum_c[kMaxAlignExperts + 1];
   unsigned long long lanes[kMaxSlots + kMaxAlignExperts];  // per bucket key: lanes of a block
   alignas(16) int stage[2][kStage];  // per side: sorted, then expert ids from round4(n)
 };
@@ -57,20 +55,29 @@ struct BlockDiv {
   __device__ __forceinline__ int pad(int x) const { return div(x + bs - 1) * bs; }
 };
 
-// Exclusive scan of block-padded counts over nb buckets; each lane owns a contiguous run.
-__device__ __forceinline__ void padded_scan(const int* cnt, int* cum, int nb, BlockDiv d) {
+// Exclusive scan of block-padded counts, 64 buckets per chunk (bucket c*64 + lane in chunk
+// c), kept in registers: ex[c] is the bucket's first position, pc[c] its padded count.
+// Returns the padded total. NC chunks cover nb buckets; chunks past nb are skipped on a
+// uniform branch. The count reads of every chunk are issued before the first scan.
+template <int NC>
+__device__ __forceinline__ int padded_scan(const int* cnt, int nb, BlockDiv d, int (&ex)[NC],
+                                           int (&pc)[NC]) {
   const int lane = __lane_id();
-  const int per = (nb + kWave - 1) / kWave;
-  const int lo = min(lane * per, nb), hi = min(lo + per, nb);
-  int local = 0;
-  for (int b = lo; b < hi; ++b) local += d.pad(cnt[b]);
-  const int incl = wave_incl_scan(local);
-  int run = incl - local;
-  for (int b = lo; b < hi; ++b) {
-    cum[b] = run;
-    run += d.pad(cnt[b]);
+  int raw[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) raw[c] = cnt[min(c * kWave + lane, nb - 1)];
+  int run = 0;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    pc[c] = c * kWave + lane < nb ? d.pad(raw[c]) : 0;
+    ex[c] = run;
+    if (c * kWave < nb) {
+      const int incl = wave_incl_scan(pc[c]);
+      ex[c] = run + incl - pc[c];
+      run += __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
   }
-  if (lane == kWave - 1) cum[nb] = incl;
+  return run;
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -104,75 +111,120 @@ __device__ __forceinline__ void copy_out(int* dst, const int* src, int n) {
   }
 }
 
-// Expert id of every block of every non-empty bucket.
-__device__ __forceinline__ void fill_eids(const int* cum, int nb, BlockDiv d, int NB,
-                                          int* eids) {
-  for (int b = __lane_id(); b < nb; b += kWave) {
-    const int q1 = min(d.div(cum[b + 1]), NB);
-    for (int q = d.div(cum[b]); q < q1; ++q) eids[q] = b;
+// Expert id of every block of every non-empty bucket, from the scan held in registers.
+template <int NC>
+__device__ __forceinline__ void fill_eids(const int (&ex)[NC], const int (&pc)[NC], int nb,
+                                          BlockDiv d, int NB, int* eids) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int b = c * kWave + lane;
+    if (b < nb) {
+      const int q1 = min(d.div(ex[c] + pc[c]), NB);
+      for (int q = d.div(ex[c]); q < q1; ++q) eids[q] = b;
+    }
   }
 }
 
-// Places each routing id at its bucket's cursor plus its rank among the earlier ids of the
-// same bucket in its block of 64, so every bucket is in token order. The lanes of a block
-// sharing a bucket are found by an atomic OR of lane bits into the bucket's mask (order-
-// free, so deterministic); a lane's rank is the popcount of the mask below it.
+// Places the ids of one block of 64 (lane -> id i, bucket key kk or -1) at their bucket's
+// cursor plus their rank among the earlier ids of the same bucket in the block, so every
+// bucket is in token order. The lanes sharing a bucket are found by an atomic OR of lane
+// bits into the bucket's mask (order-free, so deterministic; every mask starts the block at
+// zero); a lane's rank is the popcount of the mask below it. The bucket's last lane moves
+// the cursor and clears the mask for the next block.
+__device__ __forceinline__ void place_block(const AlignArgs& g, AlignLds& A, int kk, int i,
+                                            int* sorted_hot, int* sorted_cold) {
+  const int lane = __lane_id();
+  if (kk >= 0) atomicOr(&A.lanes[kk], 1ull << lane);
+  lds_sync();
+  const int kc = kk < 0 ? 0 : kk;
+  int* cur = kc >= kMaxSlots ? &A.cur_c[kc - kMaxSlots] : &A.cur_h[kc];
+  const unsigned long long m = A.lanes[kc];
+  const int c0 = *cur;
+  if (kk >= 0) {
+    const int pos = c0 + __popcll(m & lanes_below());
+    int* sorted = kk >= kMaxSlots ? sorted_cold : sorted_hot;
+    if (pos < g.L) sorted[pos] = i;
+    if ((m >> lane) == 1ull) {
+      *cur = c0 + __popcll(m);
+      A.lanes[kc] = 0ull;
+    }
+  }
+  lds_sync();
+}
+
+// Every id in token order: the first kIdRegs blocks from the keys held in registers, the
+// rest from memory.
 __device__ __forceinline__ void place_ids(const ManageArgs& a, const AlignArgs& g,
                                           const ManageLds<false>& L, AlignLds& A,
-                                          int* sorted_hot, int* sorted_cold) {
+                                          const int (&key)[kIdRegs], int* sorted_hot,
+                                          int* sorted_cold) {
   const int lane = __lane_id();
-  const int E = a.E, S = a.S, mk = a.mk;
+  const int mk = a.mk;
+#pragma unroll
+  for (int k = 0; k < kIdRegs; ++k)
+    if (k * kWave < mk) place_block(g, A, key[k], lane + k * kWave, sorted_hot, sorted_cold);
   const int* ids = reinterpret_cast<const int*>(a.ids);
-  for (int base = 0; base < mk; base += kWave) {
+  for (int base = kIdRegs * kWave; base < mk; base += kWave) {
     const int i = base + lane;
-    const int k = i < mk ? align_key(ids[i], E, S, L.tab) : -1;
-    const int kk = k < 0 ? 0 : k;
-    if (k >= 0) A.lanes[kk] = 0;
-    lds_sync();
-    if (k >= 0) atomicOr(&A.lanes[kk], 1ull << lane);
-    lds_sync();
-    int* cur = k >= kMaxSlots ? &A.cur_c[kk - kMaxSlots] : &A.cur_h[kk];
-    const unsigned long long m = A.lanes[kk];
-    const int c0 = *cur;
-    if (k >= 0) {
-      const int before = __popcll(m & lanes_below());
-      const int pos = c0 + before;
-      int* sorted = k >= kMaxSlots ? sorted_cold : sorted_hot;
-      if (pos < g.L) sorted[pos] = i;
-      if ((m >> lane) == 1ull) *cur = c0 + __popcll(m);  // the bucket's last lane moves it
-    }
-    lds_sync();
+    const int kk = i < mk ? align_key(ids[i], a.E, a.S, L.tab) : -1;
+    place_block(g, A, kk, i, sorted_hot, sorted_cold);
   }
 }
 
+template <int CS, int TQ>
 __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs& g,
-                                           const ManageLds<false>& L, AlignLds& A) {
+                                           const ManageLds<false>& L, AlignLds& A,
+                                           const long long (&idv)[kIdRegs]) {
+  // chunks of 64 buckets per side: the slots per lane cover S; the table chunks cover E up
+  // to 512, and 16 chunks cover the rest (E <= kMaxAlignExperts)
+  constexpr int CC = TQ == kTabRegs ? kMaxAlignExperts / kWave : TQ;
   const int lane = __lane_id();
   const int E = a.E, S = a.S, mk = a.mk;
   const BlockDiv d(g.bs);
   const int* ids = reinterpret_cast<const int*>(a.ids);
 
+  // bucket key of every id held in registers (the table lookups issued together)
+  int key[kIdRegs];
+#pragma unroll
+  for (int k = 0; k < kIdRegs; ++k)
+    key[k] = lane + k * kWave < mk ? align_key((int)idv[k], E, S, L.tab) : -1;
   for (int b = lane; b < S; b += kWave) A.cur_h[b] = 0;
   for (int b = lane; b < E; b += kWave) A.cur_c[b] = 0;
   lds_sync();
-  for (int i = lane; i < mk; i += kWave) {
-    const int k = align_key(ids[i], E, S, L.tab);
-    if (k >= kMaxSlots)
-      atomicAdd(&A.cur_c[k - kMaxSlots], 1);
-    else if (k >= 0)
-      atomicAdd(&A.cur_h[k], 1);
+  // counts per bucket; each used bucket's lane mask starts at zero for the placement
+#pragma unroll
+  for (int k = 0; k < kIdRegs; ++k) {
+    const int kk = key[k];
+    if (kk >= kMaxSlots)
+      atomicAdd(&A.cur_c[kk - kMaxSlots], 1);
+    else if (kk >= 0)
+      atomicAdd(&A.cur_h[kk], 1);
+    if (kk >= 0) A.lanes[kk] = 0ull;
+  }
+  for (int i = lane + kIdRegs * kWave; i < mk; i += kWave) {
+    const int kk = align_key(ids[i], E, S, L.tab);
+    if (kk >= kMaxSlots)
+      atomicAdd(&A.cur_c[kk - kMaxSlots], 1);
+    else if (kk >= 0)
+      atomicAdd(&A.cur_h[kk], 1);
+    if (kk >= 0) A.lanes[kk] = 0ull;
   }
   lds_sync();
-  padded_scan(A.cur_h, A.cum_h, S, d);
-  padded_scan(A.cur_c, A.cum_c, E, d);
-  lds_sync();
-  const int tot_h = A.cum_h[S], tot_c = A.cum_c[E];
+  int exh[CS], pch[CS], exc[CC], pcc[CC];
+  const int tot_h = padded_scan(A.cur_h, S, d, exh, pch);
+  const int tot_c = padded_scan(A.cur_c, E, d, exc, pcc);
   if (lane == 0) {
     g.npad_hot[0] = tot_h;
     g.npad_cold[0] = tot_c;
   }
-  for (int b = lane; b < S; b += kWave) A.cur_h[b] = A.cum_h[b];
-  for (int b = lane; b < E; b += kWave) A.cur_c[b] = A.cum_c[b];
+  // placement cursors start at each bucket's first position (the counts were read above)
+#pragma unroll
+  for (int c = 0; c < CS; ++c)
+    if (c * kWave + lane < S) A.cur_h[c * kWave + lane] = exh[c];
+#pragma unroll
+  for (int c = 0; c < CC; ++c)
+    if (c * kWave + lane < E) A.cur_c[c * kWave + lane] = exc[c];
 
   // Every position below a side's padded total is an id or its bucket's padding, every
   // block below it belongs to a bucket; past it the outputs hold mk and -1.
@@ -184,14 +236,14 @@ __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs&
     int* sc = A.stage[1];
     fill_i32(sh, 0, nh, mk);
     fill_i32(sc, 0, nc, mk);
-    fill_eids(A.cum_h, S, d, g.NB, sh + oh);
-    fill_eids(A.cum_c, E, d, g.NB, sc + oc);
+    fill_eids(exh, pch, S, d, g.NB, sh + oh);
+    fill_eids(exc, pcc, E, d, g.NB, sc + oc);
     fill_i32(g.sorted_hot, nh, g.L, mk);
     fill_i32(g.sorted_cold, nc, g.L, mk);
     fill_i32(g.eids_hot, qh, g.NB, -1);
     fill_i32(g.eids_cold, qc, g.NB, -1);
     lds_sync();
-    place_ids(a, g, L, A, sh, sc);  // ends with an LDS sync
+    place_ids(a, g, L, A, key, sh, sc);  // ends with an LDS sync
     copy_out(g.sorted_hot, sh, nh);
     copy_out(g.eids_hot, sh + oh, qh);
     copy_out(g.sorted_cold, sc, nc);
@@ -202,9 +254,9 @@ __device__ __forceinline__ void align_tail(const ManageArgs& a, const AlignArgs&
     fill_i32(g.sorted_cold, 0, g.L, mk);
     fill_i32(g.eids_cold, 0, g.NB, -1);
     mem_sync();  // the defaults are written before any entry below lands on them
-    fill_eids(A.cum_h, S, d, g.NB, g.eids_hot);
-    fill_eids(A.cum_c, E, d, g.NB, g.eids_cold);
-    place_ids(a, g, L, A, g.sorted_hot, g.sorted_cold);
+    fill_eids(exh, pch, S, d, g.NB, g.eids_hot);
+    fill_eids(exc, pcc, E, d, g.NB, g.eids_cold);
+    place_ids(a, g, L, A, key, g.sorted_hot, g.sorted_cold);
   }
 }
 
@@ -216,7 +268,7 @@ __global__ __launch_bounds__(kWave) void fused_k(ManageArgs a, AlignArgs g) {
   long long idv[kIdRegs];
   manage_step<CS, false, 4, TQ>(a, L, idv);
   lds_sync();
-  align_tail(a, g, L, A);
+  align_tail<CS, TQ>(a, g, L, A, idv);
 }
 
 }  // namespace ec
