@@ -272,3 +272,16 @@ def test_install_without_vllm_stays_out_of_the_way():
     log = Log()
     assert generic.install(log) is False
     assert log.said("vLLM MoE interfaces unavailable")
+
+
+def test_prefetch_refuses_a_prediction_wider_than_the_slots():
+    """Host-side prefetch rules that need no kernel: a prediction with more ids than slots
+    is refused before anything is launched, and join() with nothing pending does nothing."""
+    layer = Layer(SCALES)
+    m = Method(layer, reads=SCALE_NAMES)
+    assert arm(layer, m)[0]
+    cache = layer._expert_cache
+    assert cache.prefetch(torch.zeros(S + 1, dtype=torch.int32)) is False
+    assert cache.prefetch(torch.zeros(1, S + 1, dtype=torch.int64)) is False
+    cache.join()
+    assert cache._pf_pending is False
