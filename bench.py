@@ -354,7 +354,6 @@ def main():
         wnm.append(got)
     st.restore(final)
     man_us, gat_us, wnm = np.array(man_us), np.array(gat_us), np.array(wnm)
-    win = nseg * seg_len
     miss_launch = wnm > 0
     win_bytes = wnm.sum() * B_exp
     achieved = win_bytes / (gat_us.sum() * 1e-6) / 1e9
@@ -420,7 +419,7 @@ def main():
     cpu = None
     if args.cpu_steps > 0:
         cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
-                           policy, decay, W, dev)
+                           policy, decay, W)
 
     prefetch = None
     if not args.no_prefetch:
@@ -494,7 +493,7 @@ def main():
 
 
 def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, policy, decay,
-                 W, dev):
+                 W):
     """The CPU path on this host: the oracle's C policy (one core) decides each layer's
     misses from the same start state, and each (miss, buffer) is one hipMemcpyAsync from
     pinned host memory into the slot. Bounded sample: the first cpu_steps timed steps."""
