@@ -134,7 +134,7 @@ def run_trace(h, ids: np.ndarray, E: int, S: int, policy: int, decay: int = 64,
 def oracle_trace(ids: np.ndarray, E: int, S: int, policy: int, decay: int = 64,
                  record_state: bool = True) -> dict:
     """The oracle over every layer of ids[T, L, mk]; histories shaped like run_trace's."""
-    T, L, mk = ids.shape
+    T, L, _ = ids.shape
     nm = np.zeros((T, L), np.int32)
     miss = np.zeros((T, L, 2 * S), np.int32)
     state = np.zeros((T, L, oracle.state_words(E, S)), np.int32) if record_state else None

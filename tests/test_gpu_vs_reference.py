@@ -148,7 +148,7 @@ def store_512():
 def test_gather_vs_reference(store_512, n):
     """tests/test_policy.py:285-310: n experts per launch, miss list (j, j)."""
     ref = _ref()
-    E, S, host, src = store_512
+    _, S, host, src = store_512
     miss = torch.arange(n, dtype=torch.int32, device=gu.DEV).repeat_interleave(2)
     n_miss = torch.tensor([n], dtype=torch.int32, device=gu.DEV)
     per_expert = sum(REF_SIZES)
