@@ -160,3 +160,39 @@ def test_gather_matches_reference_kernel():
     torch.cuda.synchronize()
     for a, b in zip(mine.dst, theirs_dst):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("chunks,lanes", [(32, 1), (16, 64)])
+def test_gather_on_the_reference_suite_shape(chunks, lanes):
+    """The reference's gather suite shape (tests/test_policy.py:234-282), our own seeds: 512
+    experts, 257 slots, its six-buffer layout (1,308,800 B per expert), a warm start with
+    257 experts in slot order, 40 steps of 5 tokens x 10 distinct ids, max_distinct 128,
+    max_inserts 64, LRU. After every step each miss slab holds its expert's bytes; at the
+    end every slot written during the run does too."""
+    E, S, md, mi = 512, 257, 128, 64
+    sizes = [819200, 409600, 51200, 640, 25600, 2560]
+    store = Expertstore(E, S, sizes, seed=21)
+    hot = sorted(np.random.default_rng(23).choice(E, S, replace=False).tolist())
+    st = gu.Layers(1, E, S, miss_cap=mi, hot=hot)
+    ref = oracle.State(E, S, hot=hot, miss_cap=mi)
+    rng = np.random.default_rng(29)
+    args = store.gather_args()
+    written = {}
+    for t in range(40):
+        ids = np.concatenate([rng.choice(E, 10, replace=False) for _ in range(5)]).astype(np.int32)
+        d_ids = torch.as_tensor(ids, device=gu.DEV)
+        assert gu.manage_call(gu.lib(), st, 0, gu.ptr(d_ids), ids.size, md, mi, 0, 64) == 0
+        assert gu.lib().expert_cache_gather(*args, st.row("miss", 0), st.row("n_miss", 0),
+                                            chunks, lanes, gu.stream()) == 0
+        assert ref.manage(ids, md, mi, 0, 64) == 0
+        torch.cuda.synchronize()
+        pairs = ref.misses()
+        assert int(st.n_miss[0, 0]) == len(pairs)
+        for e, sl in pairs:
+            store.check_slot(sl, e)
+            written[sl] = e
+    assert len(written) > 64
+    se = st.slot_expert[0].cpu().numpy()
+    for sl, e in written.items():
+        assert se[sl] == e
+        store.check_slot(sl, e)
