@@ -144,3 +144,43 @@ def test_decode_step_graph_captured(monkeypatch):
         torch.cuda.synchronize()
         assert torch.equal(static_out, want), f"replay {t}"
     assert all(int(layer._expert_cache.step[0]) == 33 for layer in cached[0])
+
+
+def _forward_prefetching(layers, methods, gates, x, stats):
+    """As _forward, and before each layer's MoE, the next layer's cache is prefetched with
+    that layer's gate applied to the current hidden state (a pre-gated predictor)."""
+    for l, (layer, m, gate) in enumerate(zip(layers, methods, gates)):
+        if l + 1 < len(layers):
+            _, pred = _route(gates[l + 1], x)
+            nxt = layers[l + 1]._expert_cache
+            if nxt.prefetch(pred):
+                stats["pred"].append(pred)
+        w, ids = _route(gate, x)
+        if l > 0:
+            stats["real"].append(ids)
+        x = x + m.apply(layer, x, w, ids)
+    return x
+
+
+def test_decode_with_next_layer_prefetch_identical(monkeypatch):
+    monkeypatch.setenv("EXPERT_CACHE_SLOTS", str(S))
+    cached = _model(True)
+    full = _model(False)
+    g = torch.Generator(device=gu.DEV).manual_seed(11)
+    stats = {"pred": [], "real": []}
+    fetched = 0
+    for t in range(48):
+        x = torch.randn(2, H, device=gu.DEV, generator=g)
+        a = _forward_prefetching(*cached, x, stats)
+        b = _forward(*full, x)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"step {t}"
+        fetched += sum(int(layer._expert_cache.pf_n_miss[0]) for layer in cached[0][1:])
+    for layer in cached[0]:
+        layer._expert_cache.join()
+    hits = sum(len(set(p.flatten().tolist()) & set(r.flatten().tolist()))
+               for p, r in zip(stats["pred"], stats["real"]))
+    total = sum(len(set(r.flatten().tolist())) for r in stats["real"])
+    print(f"pre-gated prediction: {hits}/{total} routed experts predicted; "
+          f"{fetched} experts prefetched", flush=True)
+    assert fetched > 0 and hits > 0
