@@ -139,3 +139,11 @@ def test_remap_rejects_and_empty_is_a_no_op(lib):
     assert fn(P(1), -1, 4, P(1), 8, P(1), None) == -1  # n < 0
     assert fn(P(1), 4, 3, P(1), 8, P(1), None) == -1   # id_bytes not 4 or 8
     assert fn(None, 0, 4, P(1), 8, None, None) == 0    # nothing to do, no launch
+
+
+def test_prefetch_rejects(lib):
+    """expert_cache_prefetch checks its arguments on the host, before any HIP call."""
+    fn = lib.expert_cache_prefetch
+    for E, S, mi, mk in ((0, 4, 4, 1), (-1, 4, 4, 1), (8, 0, 4, 1), (8, 1025, 4, 1),
+                         (8, 4, -1, 1), (8, 4, 1025, 1), (8, 4, 4, -1)):
+        assert fn(P(1), mk, E, S, mi, *([P(1)] * 7), None) == -1, (E, S, mi, mk)
