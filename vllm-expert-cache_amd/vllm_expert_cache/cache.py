@@ -192,12 +192,12 @@ class ExpertSlotCache:
         """Start bringing the experts predicted for this layer's next step into slots.
 
         The prefetch policy step (expert_cache_prefetch: installs at stamp 0, no step
-        advance, resident predictions untouched, at most `max_inserts` installs, at most and
-        by default S)
-        runs on the current stream; the copy of what it installed runs on the device's side
-        stream, so it overlaps whatever the current stream does next. This layer's next
-        `refresh`, or `join`, makes the current stream wait for the copy. Returns False, and
-        does nothing, when the prediction has more ids than there are slots."""
+        advance, resident predictions untouched, at most `max_inserts` installs, which
+        defaults to S and is capped there) runs on the current stream. The copy of what it
+        installed runs on the device's side stream, so it overlaps whatever the current
+        stream does next. This layer's next `refresh`, or `join`, makes the current stream
+        wait for the copy. Returns False, and does nothing, when the prediction has more ids
+        than there are slots."""
         ids = pred_ids if pred_ids.dtype == torch.int32 else pred_ids.to(torch.int32)
         ids = ids.contiguous()
         mk = int(ids.numel())
