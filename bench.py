@@ -23,9 +23,10 @@ Printed (one JSON line on stdout):
                sample of the same steps
   prefetch     a window of the timed steps with and without next-layer prefetch (each
                layer's predicted experts installed by expert_cache_prefetch and copied on a
-               side stream during the previous layer), with no model compute and with a
+               side stream during an earlier layer), with no model compute and with a
                50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
-               routing: an upper bound) and 0.8 (each id wrong with probability 0.2)
+               routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one
+               and two layers ahead
 
     python bench.py [--steps K] [--warmup W] [--slots 64] [--policy lfu]
 """
@@ -573,18 +574,19 @@ def _row(t, l):
 
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
                  W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
-                 accuracies=(None, 1.0, 0.8)):
-    """Next-layer prefetch over a window of the timed steps, every run from the same start
-    state, as one captured graph per decode step:
-      without prefetch: per layer l, manage+remap(l), gather(l), compute(l);
-      with prefetch:    layer 0's prefetch first, then per layer l the prefetch of layer
-                        l+1 (policy step on the launch stream, copy on a side stream),
-                        manage+remap(l), a wait for layer l's prefetch copy, gather(l) of
-                        what is still missing, compute(l).
+                 configs=((None, 0), (1.0, 1), (0.8, 1), (1.0, 2))):
+    """Prefetch over a window of the timed steps, every run from the same start state, as
+    one captured graph per decode step. With a lookahead of d layers:
+      d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
+      d >= 1: layers 0..d-1 prefetched first, then per layer l the prefetch of layer l+d
+              (policy step on the launch stream, copy on a side stream), manage+remap(l),
+              a wait for layer l's prefetch copy, gather(l) of what is still missing,
+              compute(l).
     compute(l) stands in for the layer's attention and expert GEMMs: a spin of C us on one
     CU (C = 0: no compute, so prefetch has nothing to hide behind). The predictor is the true
     routing with each id replaced, with probability 1 - accuracy, by a random expert;
-    accuracy 1.0 is an upper bound no real predictor reaches."""
+    accuracy 1.0 is an upper bound no real predictor reaches. `configs` lists (accuracy,
+    lookahead) pairs; (None, 0) is the run without prefetch."""
     K = min(window, T - W)
     i32 = torch.int32
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
@@ -625,7 +627,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
 
-    def launch(cur, prefetch, spin):
+    def launch(cur, la, spin):
         c = ctypes.c_void_p(cur.cuda_stream)
         sd = ctypes.c_void_p(side.cuda_stream)
 
@@ -636,12 +638,14 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             done[l].record(side)
             return rc
 
-        rc = pf(0) if prefetch else 0
+        rc = 0
+        for j in range(min(la, L)):
+            rc |= pf(j)
         for l in range(L):
-            if prefetch and l + 1 < L:
-                rc |= pf(l + 1)
+            if la and l + la < L:
+                rc |= pf(l + la)
             rc |= lib.expert_cache_manage_remap(*m_args[l], c)
-            if prefetch:
+            if la:
                 cur.wait_event(done[l])
             rc |= lib.expert_cache_gather(*gr_args[l], c)
             if spin:
@@ -652,7 +656,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     out = []
     base_ms = {}
     for C in compute:
-        for q in accuracies:
+        for q, la in configs:
             if q is None:
                 pred = None
             else:
@@ -668,7 +672,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream(), q is not None, int(C * cyc_per_us))
+                launch(torch.cuda.current_stream(), la, int(C * cyc_per_us))
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             a.record()
@@ -698,6 +702,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 base_ms[C] = ms
             gbps = moved * B_exp / elapsed / 1e9
             out.append({"compute_us_per_layer": C, "predictor_accuracy": q,
+                        "lookahead_layers": la,
                         "ms_per_step": round(ms, 4),
                         "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
                         "moved_GBps": round(gbps, 3),
@@ -706,7 +711,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                         "critical_path_inserts": int(nm.sum()),
                         "real_step_hit_rate": round(1.0 - float(nm.sum()) / distinct, 5)})
             log(f"prefetch leg, compute {C} us/layer, predictor "
-                f"{'none' if q is None else q}: {ms:.3f} ms/step "
+                f"{'none' if q is None else q}, lookahead {la}: {ms:.3f} ms/step "
                 f"({base_ms[C] / ms:.3f}x), {moved} experts moved at {gbps:.2f} GB/s, "
                 f"{int(pn.sum())} prefetched ({used} used), {int(nm.sum())} on the critical "
                 f"path")
