@@ -574,19 +574,21 @@ def _row(t, l):
 
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
                  W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
-                 configs=((None, 0), (1.0, 1), (0.8, 1), (1.0, 2))):
+                 configs=((None, 0, False), (1.0, 1, False), (1.0, 1, True), (0.8, 1, True),
+                          (1.0, 2, True))):
     """Prefetch over a window of the timed steps, every run from the same start state, as
     one captured graph per decode step. With a lookahead of d layers:
       d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
-      d >= 1: layers 0..d-1 prefetched first, then per layer l the prefetch of layer l+d
-              (policy step on the launch stream, copy on a side stream), manage+remap(l),
-              a wait for layer l's prefetch copy, gather(l) of what is still missing,
-              compute(l).
+      d >= 1: layers 0..d-1 prefetched first, then per layer l the prefetch step of layer
+              l+d and manage+remap(l) -- two launches (expert_cache_prefetch, then
+              expert_cache_manage_remap) or one (expert_cache_manage_remap_prefetch) --,
+              the copy of the prefetched experts forked onto a side stream, a wait for
+              layer l's prefetch copy, gather(l) of what is still missing, compute(l).
     compute(l) stands in for the layer's attention and expert GEMMs: a spin of C us on one
     CU (C = 0: no compute, so prefetch has nothing to hide behind). The predictor is the true
     routing with each id replaced, with probability 1 - accuracy, by a random expert;
     accuracy 1.0 is an upper bound no real predictor reaches. `configs` lists (accuracy,
-    lookahead) pairs; (None, 0) is the run without prefetch."""
+    lookahead, one launch) triples; (None, 0, False) is the run without prefetch."""
     K = min(window, T - W)
     i32 = torch.int32
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
@@ -627,24 +629,30 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
 
-    def launch(cur, la, spin):
+    def launch(cur, la, one, spin):
         c = ctypes.c_void_p(cur.cuda_stream)
         sd = ctypes.c_void_p(side.cuda_stream)
 
-        def pf(l):
-            rc = lib.expert_cache_prefetch(*p_args[l], c)
+        def copy(l):
             side.wait_stream(cur)
-            rc |= lib.expert_cache_gather(*gp_args[l], sd)
+            rc = lib.expert_cache_gather(*gp_args[l], sd)
             done[l].record(side)
             return rc
 
         rc = 0
         for j in range(min(la, L)):
-            rc |= pf(j)
+            rc |= lib.expert_cache_prefetch(*p_args[j], c) | copy(j)
         for l in range(L):
-            if la and l + la < L:
-                rc |= pf(l + la)
-            rc |= lib.expert_cache_manage_remap(*m_args[l], c)
+            n = l + la
+            if la and n < L and one:
+                rc |= lib.expert_cache_manage_remap_prefetch(*m_args[l], _row(pred_static, n),
+                                                             mk, S, *p_args[n][5:], c)
+                rc |= copy(n)
+            elif la and n < L:
+                rc |= lib.expert_cache_prefetch(*p_args[n], c) | copy(n)
+                rc |= lib.expert_cache_manage_remap(*m_args[l], c)
+            else:
+                rc |= lib.expert_cache_manage_remap(*m_args[l], c)
             if la:
                 cur.wait_event(done[l])
             rc |= lib.expert_cache_gather(*gr_args[l], c)
@@ -656,7 +664,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     out = []
     base_ms = {}
     for C in compute:
-        for q, la in configs:
+        for q, la, one in configs:
             if q is None:
                 pred = None
             else:
@@ -672,7 +680,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream(), la, int(C * cyc_per_us))
+                launch(torch.cuda.current_stream(), la, one, int(C * cyc_per_us))
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             a.record()
@@ -702,7 +710,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 base_ms[C] = ms
             gbps = moved * B_exp / elapsed / 1e9
             out.append({"compute_us_per_layer": C, "predictor_accuracy": q,
-                        "lookahead_layers": la,
+                        "lookahead_layers": la, "one_launch": one,
                         "ms_per_step": round(ms, 4),
                         "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
                         "moved_GBps": round(gbps, 3),
@@ -711,7 +719,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                         "critical_path_inserts": int(nm.sum()),
                         "real_step_hit_rate": round(1.0 - float(nm.sum()) / distinct, 5)})
             log(f"prefetch leg, compute {C} us/layer, predictor "
-                f"{'none' if q is None else q}, lookahead {la}: {ms:.3f} ms/step "
+                f"{'none' if q is None else q}, lookahead {la}"
+                f"{', one launch' if one else ''}: {ms:.3f} ms/step "
                 f"({base_ms[C] / ms:.3f}x), {moved} experts moved at {gbps:.2f} GB/s, "
                 f"{int(pn.sum())} prefetched ({used} used), {int(nm.sum())} on the critical "
                 f"path")

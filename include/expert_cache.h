@@ -129,6 +129,27 @@ int expert_cache_prefetch(const int* pred_ids, int mk, int E, int S, int max_ins
                           int* table, int* map_cold, int* slot_expert, long long* slot_stamp,
                           unsigned char* routed, int* miss, int* n_miss, hipStream_t stream);
 
+/*
+ * expert_cache_manage_remap on one layer's state and expert_cache_prefetch on another's, in
+ * one launch of two workgroups: the results are exactly those of the two calls made
+ * separately (in either order). A decode step that predicts the next layer's routing before
+ * this layer's policy step puts one node on the stream for both instead of two. The pf_*
+ * arguments are expert_cache_prefetch's, for the other layer; both layers have E experts
+ * and S slots. Argument checks are those of the two calls, and it also fails with -1 when
+ * the two layers' table, map_cold, slot_expert, slot_stamp, routed, miss (2 x max_inserts
+ * ints against 2 x pf_max_inserts) or n_miss arrays overlap. No array of one layer may
+ * overlap any array of the other, since the workgroups run unordered.
+ *
+ * No counterpart in the reference's C-ABI, like expert_cache_prefetch (README.md:392-394).
+ */
+int expert_cache_manage_remap_prefetch(
+    const void* ids, int id_bytes, int mk, int E, int S, int max_distinct, int max_inserts,
+    int* table, int* map_cold, int* slot_expert, long long* slot_stamp, unsigned char* routed,
+    long long* step, int* miss, int* n_miss, int policy, int decay, void* out,
+    const int* pred_ids, int pk, int pf_max_inserts, int* pf_table, int* pf_map_cold,
+    int* pf_slot_expert, long long* pf_slot_stamp, unsigned char* pf_routed, int* pf_miss,
+    int* pf_n_miss, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,3 +147,41 @@ def test_prefetch_rejects(lib):
     for E, S, mi, mk in ((0, 4, 4, 1), (-1, 4, 4, 1), (8, 0, 4, 1), (8, 1025, 4, 1),
                          (8, 4, -1, 1), (8, 4, 1025, 1), (8, 4, 4, -1)):
         assert fn(P(1), mk, E, S, mi, *([P(1)] * 7), None) == -1, (E, S, mi, mk)
+
+
+def _manage_prefetch(h, **over):
+    """expert_cache_manage_remap_prefetch with E=8, S=4 and every array at its own address
+    (never dereferenced: each call below is rejected on the host)."""
+    a = {k: 0x100000 + i * 0x1000 for i, k in enumerate(
+        ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "miss", "n_miss"))}
+    p = {k: 0x200000 + i * 0x1000 for i, k in enumerate(
+        ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "miss", "n_miss"))}
+    v = dict(id_bytes=4, mk=1, E=8, S=4, md=1, mi=4, policy=1, out=0x300000, pk=1, pmi=4)
+    for k, x in over.items():
+        if k.startswith("a_"):
+            a[k[2:]] = x
+        elif k.startswith("p_"):
+            p[k[2:]] = x
+        else:
+            v[k] = x
+    return h.expert_cache_manage_remap_prefetch(
+        P(0x400000), v["id_bytes"], v["mk"], v["E"], v["S"], v["md"], v["mi"],
+        P(a["table"]), P(a["map_cold"]), P(a["slot_expert"]), P(a["slot_stamp"]),
+        P(a["routed"]), P(0x500000), P(a["miss"]), P(a["n_miss"]), v["policy"], 64,
+        P(v["out"]), P(0x600000), v["pk"], v["pmi"], P(p["table"]), P(p["map_cold"]),
+        P(p["slot_expert"]), P(p["slot_stamp"]), P(p["routed"]), P(p["miss"]),
+        P(p["n_miss"]), None)
+
+
+@pytest.mark.parametrize("over", [
+    dict(E=0), dict(S=0), dict(S=1025), dict(mi=-1), dict(mi=1025), dict(policy=2),
+    dict(id_bytes=2), dict(out=0), dict(pmi=-1), dict(pmi=1025), dict(pk=-1),
+    # the two layers' arrays meet: same array, or a range that reaches into the other
+    dict(p_table=0x100000), dict(p_map_cold=0x101000 + 28), dict(p_slot_expert=0x102000 - 12),
+    dict(p_slot_stamp=0x103000 + 24), dict(p_routed=0x104000 + 7), dict(p_miss=0x105000 + 28),
+    dict(p_miss=0x105000 - 28, pmi=4), dict(p_n_miss=0x106000),
+], ids=lambda d: ",".join(f"{k}={v}" for k, v in d.items()))
+def test_manage_remap_prefetch_rejects(lib, over):
+    """expert_cache_manage_remap_prefetch checks its arguments, and that the two layers'
+    arrays are disjoint, on the host before any HIP call."""
+    assert _manage_prefetch(lib, **over) == -1

@@ -146,14 +146,15 @@ def test_decode_step_graph_captured(monkeypatch):
     assert all(int(layer._expert_cache.step[0]) == 33 for layer in cached[0])
 
 
-def _forward_prefetching(layers, methods, gates, x, stats):
+def _forward_prefetching(layers, methods, gates, x, stats, along=False):
     """As _forward, and before each layer's MoE, the next layer's cache is prefetched with
-    that layer's gate applied to the current hidden state (a pre-gated predictor)."""
+    that layer's gate applied to the current hidden state (a pre-gated predictor). With
+    `along`, the prefetch step is staged to run inside this layer's policy launch."""
     for l, (layer, m, gate) in enumerate(zip(layers, methods, gates)):
         if l + 1 < len(layers):
             _, pred = _route(gates[l + 1], x)
             nxt = layers[l + 1]._expert_cache
-            if nxt.prefetch(pred):
+            if nxt.prefetch(pred, along=layer._expert_cache if along else None):
                 stats["pred"].append(pred)
         w, ids = _route(gate, x)
         if l > 0:
@@ -162,7 +163,8 @@ def _forward_prefetching(layers, methods, gates, x, stats):
     return x
 
 
-def test_decode_with_next_layer_prefetch_identical(monkeypatch):
+@pytest.mark.parametrize("along", [False, True], ids=["own-launch", "along"])
+def test_decode_with_next_layer_prefetch_identical(monkeypatch, along):
     monkeypatch.setenv("EXPERT_CACHE_SLOTS", str(S))
     cached = _model(True)
     full = _model(False)
@@ -171,7 +173,7 @@ def test_decode_with_next_layer_prefetch_identical(monkeypatch):
     fetched = 0
     for t in range(48):
         x = torch.randn(2, H, device=gu.DEV, generator=g)
-        a = _forward_prefetching(*cached, x, stats)
+        a = _forward_prefetching(*cached, x, stats, along)
         b = _forward(*full, x)
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"step {t}"
@@ -184,3 +186,38 @@ def test_decode_with_next_layer_prefetch_identical(monkeypatch):
     print(f"pre-gated prediction: {hits}/{total} routed experts predicted; "
           f"{fetched} experts prefetched", flush=True)
     assert fetched > 0 and hits > 0
+
+
+def test_decode_with_prefetch_along_graph_captured(monkeypatch):
+    """The pre-gated decode step with every prefetch staged along the layer before, captured
+    in one graph: each layer's policy launch carries the next layer's prefetch step."""
+    monkeypatch.setenv("EXPERT_CACHE_SLOTS", str(S))
+    cached = _model(True)
+    full = _model(False)
+    static_x = torch.zeros(2, H, device=gu.DEV)
+    stats = {"pred": [], "real": []}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _forward_prefetching(*cached, static_x, stats, along=True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = _forward_prefetching(*cached, static_x, stats, along=True)
+    caches = [layer._expert_cache for layer in cached[0]]
+    assert all(c._rider is None and c._riding_on is None and not c._pf_pending
+               for c in caches)
+    g = torch.Generator(device=gu.DEV).manual_seed(7)
+    for t in range(32):
+        static_x.copy_(torch.randn(2, H, device=gu.DEV, generator=g))
+        graph.replay()
+        want = _forward(*full, static_x.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, want), f"replay {t}"
+    assert all(int(c.step[0]) == 33 for c in caches)
+    for c, layer in zip(caches, cached[0]):
+        resident = c.slot_expert[c.slot_expert >= 0].long()
+        for n in ("w13_weight", "w2_weight"):
+            assert torch.equal(c.slots[n][c.slot_expert >= 0],
+                               getattr(layer, n).data[resident]), n

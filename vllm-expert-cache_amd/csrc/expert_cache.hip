@@ -23,6 +23,13 @@ namespace {
 // through the expert in order, each workgroup taking every grid-th tile.
 constexpr int kGatherUnroll = 2;
 
+// [p, p + pn) and [q, q + qn) share a byte
+bool ranges_meet(const void* p, long long pn, const void* q, long long qn) {
+  const long long a = (long long)reinterpret_cast<uintptr_t>(p);
+  const long long b = (long long)reinterpret_cast<uintptr_t>(q);
+  return pn > 0 && qn > 0 && a < b + qn && b < a + pn;
+}
+
 bool manage_args_bad(int E, int S, int max_inserts, int policy) {
   if (E <= 0 || S <= 0 || S > kMaxSlots || S > kSlotMask) return true;
   if (max_inserts < 0 || max_inserts > kMaxInserts) return true;
@@ -89,6 +96,38 @@ int launch_prefetch(const ManageArgs& a, hipStream_t stream) {
     case 2: return launch_prefetch_tq<2>(a, stream);
     case 4: return launch_prefetch_tq<4>(a, stream);
     default: return launch_prefetch_tq<kTabRegs>(a, stream);
+  }
+}
+
+// Both layers share E and S, so one variant serves the two workgroups.
+template <int IDB, int TQ>
+int launch_manage_prefetch_tq(const ManageArgs& a, const ManageArgs& p, hipStream_t stream) {
+  const dim3 grid(2), block(kWave);
+  if (a.S <= 64)
+    hipLaunchKernelGGL((manage_prefetch_k<1, false, IDB, TQ>), grid, block, 0, stream, a, p);
+  else if (a.S <= 128)
+    hipLaunchKernelGGL((manage_prefetch_k<2, false, IDB, TQ>), grid, block, 0, stream, a, p);
+  else if (a.S <= 256)
+    hipLaunchKernelGGL((manage_prefetch_k<4, false, IDB, TQ>), grid, block, 0, stream, a, p);
+  else if (a.S <= 512)
+    hipLaunchKernelGGL((manage_prefetch_k<8, false, IDB, TQ>), grid, block, 0, stream, a, p);
+  else
+    hipLaunchKernelGGL((manage_prefetch_k<16, false, IDB, TQ>), grid, block, 0, stream, a, p);
+  return (int)hipGetLastError();
+}
+
+template <int IDB>
+int launch_manage_prefetch(const ManageArgs& a, const ManageArgs& p, hipStream_t stream) {
+  if (a.E > kLdsExperts) {
+    hipLaunchKernelGGL((manage_prefetch_k<16, true, IDB, kTabRegs>), dim3(2), dim3(kWave), 0,
+                       stream, a, p);
+    return (int)hipGetLastError();
+  }
+  switch (table_chunks(a.E)) {
+    case 1: return launch_manage_prefetch_tq<IDB, 1>(a, p, stream);
+    case 2: return launch_manage_prefetch_tq<IDB, 2>(a, p, stream);
+    case 4: return launch_manage_prefetch_tq<IDB, 4>(a, p, stream);
+    default: return launch_manage_prefetch_tq<IDB, kTabRegs>(a, p, stream);
   }
 }
 
@@ -183,6 +222,36 @@ int expert_cache_prefetch(const int* pred_ids, int mk, int E, int S, int max_ins
                                  slot_expert, slot_stamp, routed, nullptr, miss, n_miss, 0, 0,
                                  nullptr);
   return launch_prefetch(a, stream);
+}
+
+int expert_cache_manage_remap_prefetch(
+    const void* ids, int id_bytes, int mk, int E, int S, int max_distinct, int max_inserts,
+    int* table, int* map_cold, int* slot_expert, long long* slot_stamp, unsigned char* routed,
+    long long* step, int* miss, int* n_miss, int policy, int decay, void* out,
+    const int* pred_ids, int pk, int pf_max_inserts, int* pf_table, int* pf_map_cold,
+    int* pf_slot_expert, long long* pf_slot_stamp, unsigned char* pf_routed, int* pf_miss,
+    int* pf_n_miss, hipStream_t stream) {
+  if (manage_args_bad(E, S, max_inserts, policy)) return -1;
+  if (id_bytes != 4 && id_bytes != 8) return -1;
+  if (mk > 0 && out == nullptr) return -1;
+  if (manage_args_bad(E, S, pf_max_inserts, 0) || pk < 0) return -1;
+  // the two workgroups run unordered: the layers must not share any array
+  const long long e4 = 4LL * E, s4 = 4LL * S;
+  if (ranges_meet(table, e4, pf_table, e4) || ranges_meet(map_cold, e4, pf_map_cold, e4) ||
+      ranges_meet(slot_expert, s4, pf_slot_expert, s4) ||
+      ranges_meet(slot_stamp, 2 * s4, pf_slot_stamp, 2 * s4) ||
+      ranges_meet(routed, E, pf_routed, E) ||
+      ranges_meet(miss, 8LL * max_inserts, pf_miss, 8LL * pf_max_inserts) ||
+      ranges_meet(n_miss, 4, pf_n_miss, 4))
+    return -1;
+  const ManageArgs a = make_args(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                 slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
+                                 decay, out);
+  const ManageArgs p = make_args(pred_ids, pk, E, S, E, pf_max_inserts, pf_table, pf_map_cold,
+                                 pf_slot_expert, pf_slot_stamp, pf_routed, nullptr, pf_miss,
+                                 pf_n_miss, 0, 0, nullptr);
+  return id_bytes == 8 ? launch_manage_prefetch<8>(a, p, stream)
+                       : launch_manage_prefetch<4>(a, p, stream);
 }
 
 int expert_cache_remap(const void* ids, int n, int id_bytes, const int* table, int E,

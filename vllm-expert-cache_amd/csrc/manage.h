@@ -574,6 +574,26 @@ __global__ __launch_bounds__(kWave) void prefetch_k(ManageArgs a) {
   manage_step<CS, GLOBAL_E, 4, TQ, true>(a, L, idv);
 }
 
+// Two workgroups, two layers: workgroup 0 runs layer a's policy step and remap (manage_k
+// with REMAP), workgroup 1 the prefetch step of another layer p (prefetch_k). The host
+// rejects states that share arrays, so the workgroups touch disjoint memory and need no
+// ordering between them; the pair occupies one node of the stream instead of two.
+template <int CS, bool GLOBAL_E, int IDB, int TQ>
+__global__ __launch_bounds__(kWave) void manage_prefetch_k(ManageArgs a, ManageArgs p) {
+  __shared__ ManageLds<GLOBAL_E> L;
+  long long idv[kIdRegs];
+  if (blockIdx.x == 0) {
+    args_in_sgprs(a);
+    manage_step<CS, GLOBAL_E, IDB, TQ>(a, L, idv);
+    if constexpr (GLOBAL_E) mem_sync();
+    else lds_sync();
+    remap_tail<GLOBAL_E, IDB>(a, L, idv);
+  } else {
+    args_in_sgprs(p);
+    manage_step<CS, GLOBAL_E, 4, TQ, true>(p, L, idv);
+  }
+}
+
 // Standalone remap, any grid; one id per lane per iteration.
 template <int IDB>
 __global__ __launch_bounds__(256) void remap_k(const void* ids, int n, const int* table, int E,

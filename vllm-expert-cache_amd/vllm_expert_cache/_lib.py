@@ -1,11 +1,12 @@
 """ctypes binding of libexpertcache.so (C-ABI in include/expert_cache.h).
 
 Same search order and same argument lists for the reference's two bound entry points
-(vllm_expert_cache/_lib.py:15-61): manage and gather. Four more are bound here:
+(vllm_expert_cache/_lib.py:15-61): manage and gather. Five more are bound here:
 `expert_cache_fused` (exported by the reference but never bound), the two remap entry
-points that replace the reference's torch remap, and `expert_cache_prefetch`. Every call is
-asynchronous on the caller's stream and never reads a device value back, so the whole path
-is HIP-graph capturable.
+points that replace the reference's torch remap, `expert_cache_prefetch`, and
+`expert_cache_manage_remap_prefetch` (one layer's policy step with another's prefetch step
+in one launch). Every call is asynchronous on the caller's stream and never reads a device
+value back, so the whole path is HIP-graph capturable.
 
 There is no fallback: if the library or one of its symbols is missing, loading fails with
 an error that says so.
@@ -45,6 +46,11 @@ SIGNATURES = {
     # prefetch(pred_ids, mk, E, S, max_inserts, table, map_cold, slot_expert, slot_stamp,
     #          routed, miss, n_miss, stream)
     "expert_cache_prefetch": [_P] + [_I] * 4 + [_P] * 7 + [_P],
+    # manage_remap_prefetch(manage_remap args without stream, pred_ids, pk, pf_max_inserts,
+    #                       pf_table, pf_map_cold, pf_slot_expert, pf_slot_stamp, pf_routed,
+    #                       pf_miss, pf_n_miss, stream)
+    "expert_cache_manage_remap_prefetch": ([_P] + [_I] * 6 + [_P] * 8 + [_I, _I, _P]
+                                           + [_P, _I, _I] + [_P] * 7 + [_P]),
 }
 
 

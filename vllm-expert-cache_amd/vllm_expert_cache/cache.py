@@ -18,8 +18,10 @@ without talking to each other.
 A caller that can predict a layer's next routing (for instance from the previous layer's
 hidden state) calls `prefetch` early: the install-only policy step runs on the current
 stream and the copy of the predicted experts on a side stream, overlapping what follows;
-the layer's next `refresh` waits for that copy before its own gather. README.md:392-394 of
-the reference names this as the path's next step.
+the layer's next `refresh` waits for that copy before its own gather. With `along=` another
+layer's cache, the prefetch step waits for that layer's next `refresh` and runs inside the
+same launch as its policy step (expert_cache_manage_remap_prefetch), one stream node instead
+of two. README.md:392-394 of the reference names prefetch as the path's next step.
 
 Constructor, attributes and methods mirror vllm_expert_cache/cache.py:38-163 of the
 reference (`fits`, `remap`, `refresh`, `slots`, `bound`, `names`, `skipped`, `E`, `S`).
@@ -135,6 +137,10 @@ class ExpertSlotCache:
         self.pf_n_miss = torch.zeros((1,), dtype=i32, device=device)
         self._pf_done = None
         self._pf_pending = False
+        # prefetch staged to ride with this cache's next policy launch: (cache, ids, budget)
+        self._rider = None
+        # the cache whose next policy launch carries this cache's staged prefetch
+        self._riding_on = None
 
         self.policy = settings.policy_code
         self.decay = settings.decay
@@ -169,26 +175,39 @@ class ExpertSlotCache:
         return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
 
     def refresh(self, topk_ids: torch.Tensor) -> torch.Tensor:
-        """Run the policy step and the gather for this step; return slot-space ids."""
+        """Run the policy step and the gather for this step; return slot-space ids. A
+        prefetch staged with `along=self` runs in the same launch as the policy step."""
         h = lib()
+        if self._riding_on is not None:  # this layer's own staged prefetch goes first
+            self._riding_on._flush_rider()
         stream = self._stream()
         ids, nbytes = self._id_view(topk_ids)
         out = torch.empty_like(ids)
         mk = int(ids.numel())
-
-        rc = h.expert_cache_manage_remap(
-            _ptr(ids), nbytes, mk, self.E, self.S, min(self.E, mk), self.S,
-            _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
-            _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.step), _ptr(self.miss),
-            _ptr(self.n_miss), self.policy, self.decay, _ptr(out), stream)
+        own = (_ptr(ids), nbytes, mk, self.E, self.S, min(self.E, mk), self.S,
+               _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
+               _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.step), _ptr(self.miss),
+               _ptr(self.n_miss), self.policy, self.decay, _ptr(out))
+        rider = self._rider
+        if rider is None:
+            rc = h.expert_cache_manage_remap(*own, stream)
+        else:
+            other, pred, budget = rider
+            self._rider = other._riding_on = None
+            other._wait_copy()  # its previous copy may still read pf_miss
+            rc = h.expert_cache_manage_remap_prefetch(
+                *own, _ptr(pred), int(pred.numel()), budget, *other._pf_state(), stream)
         if rc != 0:
             raise RuntimeError(f"expert_cache_manage failed rc={rc}")
+        if rider is not None:
+            rider[0]._copy_prefetched()
         # a prefetched slot may be this step's victim: its copy lands before this gather
-        self.join()
+        self._wait_copy()
         self._gather(self.miss, self.n_miss, stream)
         return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
 
-    def prefetch(self, pred_ids: torch.Tensor, max_inserts: int | None = None) -> bool:
+    def prefetch(self, pred_ids: torch.Tensor, max_inserts: int | None = None,
+                 along: "ExpertSlotCache | None" = None) -> bool:
         """Start bringing the experts predicted for this layer's next step into slots.
 
         The prefetch policy step (expert_cache_prefetch: installs at stamp 0, no step
@@ -197,22 +216,71 @@ class ExpertSlotCache:
         installed runs on the device's side stream, so it overlaps whatever the current
         stream does next. This layer's next `refresh`, or `join`, makes the current stream
         wait for the copy. Returns False, and does nothing, when the prediction has more ids
-        than there are slots."""
+        than there are slots.
+
+        With `along` (another layer's cache on the same device, with the same experts and
+        slots), the policy step is staged instead: it runs inside the same launch as
+        `along`'s next policy step, at its next `refresh`, and its copy is forked from
+        there. The prediction's values are read at that launch. `along.join()`, or any
+        call on this cache that reads the policy state (`refresh`, `join`, `prefetch`),
+        launches a staged step on its own first."""
         ids = pred_ids if pred_ids.dtype == torch.int32 else pred_ids.to(torch.int32)
         ids = ids.contiguous()
         mk = int(ids.numel())
         if mk > self.S:
             return False
-        self.join()  # the previous copy may still read pf_miss
+        budget = self.S if max_inserts is None else min(int(max_inserts), self.S)
+        if self._riding_on is not None:  # an earlier staged step comes first
+            self._riding_on._flush_rider()
+        if along is None:
+            self._wait_copy()  # the previous copy may still read pf_miss
+            cur = torch.cuda.current_stream(self.table.device)
+            rc = lib().expert_cache_prefetch(_ptr(ids), mk, self.E, self.S, budget,
+                                             *self._pf_state(),
+                                             ctypes.c_void_p(cur.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"expert_cache_prefetch failed rc={rc}")
+            self._copy_prefetched()
+            return True
+        if along is self or (along.E, along.S) != (self.E, self.S) or \
+                along.table.device != self.table.device:
+            raise ValueError("prefetch along= needs another layer's cache on the same device "
+                             "with the same experts and slots")
+        if along._rider is not None:
+            along._flush_rider()
+        along._rider = (self, ids, budget)
+        self._riding_on = along
+        return True
+
+    def join(self) -> None:
+        """Make the current stream wait for this layer's pending prefetch copy, if any.
+        A prefetch staged on or with this cache is launched first, on its own."""
+        if self._rider is not None:
+            self._flush_rider()
+        if self._riding_on is not None:
+            self._riding_on._flush_rider()
+        self._wait_copy()
+
+    def _wait_copy(self) -> None:
+        if self._pf_pending:
+            torch.cuda.current_stream(self.table.device).wait_event(self._pf_done)
+            self._pf_pending = False
+
+    def _flush_rider(self) -> None:
+        """Launch the prefetch staged on this cache on its own."""
+        other, pred, budget = self._rider
+        self._rider = other._riding_on = None
+        other.prefetch(pred, budget)
+
+    def _pf_state(self) -> tuple:
+        """The prefetch step's state and miss-list arguments, in C-ABI order."""
+        return (_ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
+                _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.pf_miss),
+                _ptr(self.pf_n_miss))
+
+    def _copy_prefetched(self) -> None:
+        """Fork the copy of what the prefetch step just installed onto the side stream."""
         cur = torch.cuda.current_stream(self.table.device)
-        rc = lib().expert_cache_prefetch(
-            _ptr(ids), mk, self.E, self.S,
-            self.S if max_inserts is None else min(int(max_inserts), self.S),
-            _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
-            _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.pf_miss),
-            _ptr(self.pf_n_miss), ctypes.c_void_p(cur.cuda_stream))
-        if rc != 0:
-            raise RuntimeError(f"expert_cache_prefetch failed rc={rc}")
         side = _side_stream(self.table.device)
         side.wait_stream(cur)
         self._gather(self.pf_miss, self.pf_n_miss, ctypes.c_void_p(side.cuda_stream))
@@ -220,13 +288,6 @@ class ExpertSlotCache:
             self._pf_done = torch.cuda.Event()
         self._pf_done.record(side)
         self._pf_pending = True
-        return True
-
-    def join(self) -> None:
-        """Make the current stream wait for this layer's pending prefetch copy, if any."""
-        if self._pf_pending:
-            torch.cuda.current_stream(self.table.device).wait_event(self._pf_done)
-            self._pf_pending = False
 
     def _gather(self, miss: torch.Tensor, n_miss: torch.Tensor, stream) -> None:
         """expert_cache_gather of every mirrored tensor over one miss list, six per call."""
