@@ -6,7 +6,8 @@ values, max_distinct (including below the routed count: read-through), max_inser
 (including 0 and caps below the miss count), policy and decay, and a random consistent warm
 state with random stamps. Each step is compared on every field, and the fused remap output
 against the closed form. The prefetch step runs over the same space, interleaved with
-manage steps.
+manage steps, and so does the one-launch pair of a policy step on one layer and a prefetch
+step on another.
 """
 from __future__ import annotations
 
@@ -162,3 +163,70 @@ def test_random_prefetch(seed):
                           ("miss", st.miss[0]), ("n_miss", st.n_miss[0])):
             got, want = dev.cpu().numpy(), getattr(ref, name)
             assert np.array_equal(got, want), f"{tag} (manage): {name} differs at {gu.first_diff(got, want)}"
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_one_launch(seed):
+    """expert_cache_manage_remap_prefetch over the same random space: two layers with the
+    same E and S and their own warm states; each step one layer's policy step and remap
+    (int32 or int64 ids, any max_distinct) and the other layer's prefetch (any ids, any
+    budget) run as one launch, and both layers are compared on every field."""
+    rng, E, S, mk, mi, policy, decay, hot, slots, stamps = _case(9000 + seed)
+    layers = [_device_state(E, S, mi, hot, slots, stamps)]
+    nhot = int(rng.integers(0, min(S, E) + 1))
+    layers.append(_device_state(E, S, mi, rng.choice(E, nhot, replace=False),
+                                rng.choice(S, nhot, replace=False),
+                                rng.integers(0, 1000, size=S)))
+    pcap = 1024
+    pf = [(torch.zeros((2 * pcap,), dtype=torch.int32, device=gu.DEV),
+           torch.zeros((1,), dtype=torch.int32, device=gu.DEV)) for _ in range(2)]
+    ref_pf = [(np.zeros(2 * pcap, np.int32), np.zeros(1, np.int32)) for _ in range(2)]
+    side = oracle.State(E, S, miss_cap=pcap)  # carries a prefetch's miss list
+    for t in range(STEPS):
+        j = int(rng.integers(0, 2))
+        k = 1 - j
+        (st_j, ref_j), (st_k, ref_k) = layers[j], layers[k]
+        ids = rng.integers(-3, E + 3, size=mk).astype(np.int32)
+        distinct = len(np.unique(ids[(ids >= 0) & (ids < E)]))
+        md = int(rng.choice([distinct, distinct - 1, E, mk]))
+        idb = int(rng.choice([4, 8]))
+        d_ids = torch.as_tensor(ids.astype(np.int64 if idb == 8 else np.int32), device=gu.DEV)
+        out = torch.full((max(mk, 1),), -9, dtype=d_ids.dtype, device=gu.DEV)
+        pk = int(rng.choice([0, 1, 8, mk, 300]))
+        budget = int(rng.choice([0, 1, 4, S, 1024]))
+        pred = rng.integers(-3, E + 3, size=pk).astype(np.int32)
+        d_pred = torch.as_tensor(pred, device=gu.DEV)
+        rc = gu.lib().expert_cache_manage_remap_prefetch(
+            gu.ptr(d_ids) if mk else None, idb, mk, E, S, md, mi, st_j.row("table", 0),
+            st_j.row("map_cold", 0), st_j.row("slot_expert", 0), st_j.row("slot_stamp", 0),
+            st_j.row("routed", 0), st_j.row("step", 0), st_j.row("miss", 0),
+            st_j.row("n_miss", 0), policy, decay, gu.ptr(out), gu.ptr(d_pred) if pk else None,
+            pk, budget, st_k.row("table", 0), st_k.row("map_cold", 0),
+            st_k.row("slot_expert", 0), st_k.row("slot_stamp", 0), st_k.row("routed", 0),
+            gu.ptr(pf[k][0]), gu.ptr(pf[k][1]), gu.stream())
+        assert rc == 0
+        assert ref_j.manage(ids, md, mi, policy, decay) == 0
+        for f in ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "step"):
+            setattr(side, f, getattr(ref_k, f))  # shared arrays: one state, two miss lists
+        side.miss[:], side.n_miss[:] = ref_pf[k]
+        assert side.prefetch(pred, budget) == 0
+        ref_pf[k] = side.miss.copy(), side.n_miss.copy()
+        torch.cuda.synchronize()
+        tag = (f"seed {seed} step {t}: E={E} S={S} mk={mk} md={md} mi={mi} id{8 * idb} "
+               f"pk={pk} budget={budget} manage on layer {j}")
+        for l, (st, ref) in enumerate(layers):
+            for name, dev in (("table", st.table[0]), ("map_cold", st.map_cold[0]),
+                              ("slot_expert", st.slot_expert[0]),
+                              ("slot_stamp", st.slot_stamp[0]), ("routed", st.routed[0]),
+                              ("step", st.step[0]), ("miss", st.miss[0]),
+                              ("n_miss", st.n_miss[0])):
+                got, want = dev.cpu().numpy(), getattr(ref, name)
+                assert np.array_equal(got, want), \
+                    f"{tag}: layer {l} {name} differs at {gu.first_diff(got, want)}"
+            for name, dev, want in (("pf_miss", pf[l][0], ref_pf[l][0]),
+                                    ("pf_n", pf[l][1], ref_pf[l][1])):
+                got = dev.cpu().numpy()
+                assert np.array_equal(got, want), \
+                    f"{tag}: layer {l} {name} differs at {gu.first_diff(got, want)}"
+        if mk:
+            assert np.array_equal(out.cpu().numpy()[:mk], oracle.remap(ids, ref_j.table)), tag
