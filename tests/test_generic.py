@@ -285,3 +285,31 @@ def test_prefetch_refuses_a_prediction_wider_than_the_slots():
     assert cache.prefetch(torch.zeros(1, S + 1, dtype=torch.int64)) is False
     cache.join()
     assert cache._pf_pending is False
+
+
+def test_prefetch_along_stages_without_launching(monkeypatch):
+    """Staging a prefetch along another layer's cache is host bookkeeping only: nothing is
+    launched until that layer's refresh (or a join). Partners that cannot share one launch
+    are refused: the same cache, or one with other expert or slot counts."""
+    from vllm_expert_cache import cache as cache_mod
+
+    def no_launch():
+        raise AssertionError("staging must not call the library")
+
+    monkeypatch.setattr(cache_mod, "lib", no_launch)
+    layers = [Layer(SCALES), Layer(SCALES)]
+    for layer in layers:
+        assert arm(layer, Method(layer, reads=SCALE_NAMES))[0]
+    a, b = (layer._expert_cache for layer in layers)
+    pred = torch.zeros(2, dtype=torch.int32)
+    assert b.prefetch(pred, along=a) is True
+    assert a._rider[0] is b and b._riding_on is a
+    assert a._rider[2] == b.S  # budget defaults to S
+    # a prediction wider than the slots is refused before anything is staged or launched
+    assert a.prefetch(torch.zeros(a.S + 1, dtype=torch.int32), along=b) is False
+    assert b._rider is None and a._riding_on is None
+    with pytest.raises(ValueError):
+        a.prefetch(pred, along=a)
+    small = cache_mod.ExpertSlotCache(layers[0], ["w13_weight"], a.E, a.S - 1, "cpu")
+    with pytest.raises(ValueError):
+        small.prefetch(pred, along=a)
