@@ -120,3 +120,31 @@ def test_refresh_under_graph_capture():
         for n in NAMES:
             assert torch.equal(graphed.slots[n], eager.slots[n]), (t, n)
         _check_slots(graphed, owner, static_ids, static_out)
+
+
+def test_refresh_follows_a_source_that_moves():
+    """vLLM's offloader may rebind an expert tensor after the cache was built. The next
+    refresh must gather from where the tensor is now: new misses hold the new source's
+    bytes. A source moved to host memory the GPU cannot read is refused."""
+    owner = Owner(7)
+    cache = ExpertSlotCache(owner, NAMES, E, S, gu.DEV)
+    first = torch.arange(0, K, dtype=torch.int32, device=gu.DEV)
+    cache.refresh(first)
+    torch.cuda.synchronize()
+    _check_slots(cache, owner, first, cache.remap(first))
+    key = cache._gather_key
+    moved = torch.empty_like(owner.w13_weight, pin_memory=True)
+    moved.copy_(torch.randint(-128, 128, tuple(moved.shape), dtype=torch.int8))
+    owner.w13_weight = moved
+    second = torch.arange(K, 2 * K, dtype=torch.int32, device=gu.DEV)
+    slot_ids = cache.refresh(second)
+    torch.cuda.synchronize()
+    assert cache._gather_key != key
+    _check_slots(cache, owner, second, slot_ids)
+    owner.w13_weight = moved.clone()  # pageable
+    before = {f: getattr(cache, f).clone() for f in ("table", "slot_expert", "slot_stamp", "step")}
+    with pytest.raises(ValueError, match="pin it"):
+        cache.refresh(torch.arange(2 * K, 3 * K, dtype=torch.int32, device=gu.DEV))
+    torch.cuda.synchronize()
+    for f, t in before.items():  # refused before the policy step ran
+        assert torch.equal(getattr(cache, f), t), f

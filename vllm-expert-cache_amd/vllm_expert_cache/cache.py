@@ -69,18 +69,25 @@ _HIP = None
 def device_address(t: torch.Tensor) -> int:
     """Address at which the GPU reads `t`: its own for a device tensor (vLLM's offloader
     hands over device views of host memory), or the device mapping of page-locked host
-    memory from hipHostGetDevicePointer for a pinned CPU tensor."""
+    memory from hipHostGetDevicePointer for a pinned CPU tensor. Pageable memory is refused
+    before any HIP call: a failed lookup would leave an error that the next GPU call
+    reports."""
     if t.is_cuda:
         return t.data_ptr()
+    if not t.is_pinned():
+        raise ValueError(f"expert source at {t.data_ptr():#x} is pageable host memory the "
+                         f"GPU cannot read; pin it")
     global _HIP
     if _HIP is None:
         _HIP = ctypes.CDLL("libamdhip64.so")
         _HIP.hipHostGetDevicePointer.restype = ctypes.c_int
         _HIP.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p),
                                                  ctypes.c_void_p, ctypes.c_uint]
+        _HIP.hipGetLastError.restype = ctypes.c_int
     out = ctypes.c_void_p()
     rc = _HIP.hipHostGetDevicePointer(ctypes.byref(out), ctypes.c_void_p(t.data_ptr()), 0)
     if rc != 0 or not out.value:
+        _HIP.hipGetLastError()  # clear it: the caller gets the error here, not later
         raise ValueError(f"expert source at {t.data_ptr():#x} is host memory the GPU cannot "
                          f"read (hipHostGetDevicePointer rc={rc}); pin it")
     return out.value
@@ -135,12 +142,23 @@ class ExpertSlotCache:
         # step writes `miss`
         self.pf_miss = torch.zeros((2 * self.S,), dtype=i32, device=device)
         self.pf_n_miss = torch.zeros((1,), dtype=i32, device=device)
-        self._pf_done = None
+        self._pf_fork = self._pf_done = None
         self._pf_pending = False
         # prefetch staged to ride with this cache's next policy launch: (cache, ids, budget)
         self._rider = None
         # the cache whose next policy launch carries this cache's staged prefetch
         self._riding_on = None
+        # addresses every step passes to the library, fixed for the cache's lifetime (ctypes
+        # converts the ints); the gather calls are rebuilt only when a source moves
+        self._state = tuple(t.data_ptr() for t in (
+            self.table, self.map_cold, self.slot_expert, self.slot_stamp, self.routed,
+            self.step, self.miss, self.n_miss))
+        self._pf_state = tuple(t.data_ptr() for t in (
+            self.table, self.map_cold, self.slot_expert, self.slot_stamp, self.routed,
+            self.pf_miss, self.pf_n_miss))
+        self._gather_key = None
+        self._gather_srcs = ()
+        self._gather_calls = ()
 
         self.policy = settings.policy_code
         self.decay = settings.decay
@@ -180,14 +198,15 @@ class ExpertSlotCache:
         h = lib()
         if self._riding_on is not None:  # this layer's own staged prefetch goes first
             self._riding_on._flush_rider()
+        self._plan()  # a source the GPU cannot read is refused before the state changes
+        if self._rider is not None:
+            self._rider[0]._plan()
         stream = self._stream()
         ids, nbytes = self._id_view(topk_ids)
         out = torch.empty_like(ids)
         mk = int(ids.numel())
-        own = (_ptr(ids), nbytes, mk, self.E, self.S, min(self.E, mk), self.S,
-               _ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
-               _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.step), _ptr(self.miss),
-               _ptr(self.n_miss), self.policy, self.decay, _ptr(out))
+        own = (ids.data_ptr(), nbytes, mk, self.E, self.S, min(self.E, mk), self.S,
+               *self._state, self.policy, self.decay, out.data_ptr())
         rider = self._rider
         if rider is None:
             rc = h.expert_cache_manage_remap(*own, stream)
@@ -196,7 +215,7 @@ class ExpertSlotCache:
             self._rider = other._riding_on = None
             other._wait_copy()  # its previous copy may still read pf_miss
             rc = h.expert_cache_manage_remap_prefetch(
-                *own, _ptr(pred), int(pred.numel()), budget, *other._pf_state(), stream)
+                *own, pred.data_ptr(), int(pred.numel()), budget, *other._pf_state, stream)
         if rc != 0:
             raise RuntimeError(f"expert_cache_manage failed rc={rc}")
         if rider is not None:
@@ -233,11 +252,11 @@ class ExpertSlotCache:
         if self._riding_on is not None:  # an earlier staged step comes first
             self._riding_on._flush_rider()
         if along is None:
+            self._plan()
             self._wait_copy()  # the previous copy may still read pf_miss
             cur = torch.cuda.current_stream(self.table.device)
-            rc = lib().expert_cache_prefetch(_ptr(ids), mk, self.E, self.S, budget,
-                                             *self._pf_state(),
-                                             ctypes.c_void_p(cur.cuda_stream))
+            rc = lib().expert_cache_prefetch(ids.data_ptr(), mk, self.E, self.S, budget,
+                                             *self._pf_state, cur.cuda_stream)
             if rc != 0:
                 raise RuntimeError(f"expert_cache_prefetch failed rc={rc}")
             self._copy_prefetched()
@@ -272,38 +291,51 @@ class ExpertSlotCache:
         self._rider = other._riding_on = None
         other.prefetch(pred, budget)
 
-    def _pf_state(self) -> tuple:
-        """The prefetch step's state and miss-list arguments, in C-ABI order."""
-        return (_ptr(self.table), _ptr(self.map_cold), _ptr(self.slot_expert),
-                _ptr(self.slot_stamp), _ptr(self.routed), _ptr(self.pf_miss),
-                _ptr(self.pf_n_miss))
-
     def _copy_prefetched(self) -> None:
         """Fork the copy of what the prefetch step just installed onto the side stream."""
         cur = torch.cuda.current_stream(self.table.device)
         side = _side_stream(self.table.device)
-        side.wait_stream(cur)
-        self._gather(self.pf_miss, self.pf_n_miss, ctypes.c_void_p(side.cuda_stream))
-        if self._pf_done is None:
-            self._pf_done = torch.cuda.Event()
+        if self._pf_done is None:  # two events per cache, re-recorded every prefetch
+            self._pf_fork, self._pf_done = torch.cuda.Event(), torch.cuda.Event()
+        self._pf_fork.record(cur)
+        side.wait_event(self._pf_fork)
+        self._gather(self.pf_miss, self.pf_n_miss, side.cuda_stream)
         self._pf_done.record(side)
         self._pf_pending = True
 
+    def _plan(self) -> None:
+        """Resolve the gather calls against where the sources are now. vLLM's offloader
+        may rebind them after the cache is built, so they are re-read every step, and the
+        calls are rebuilt when one moved."""
+        srcs = tuple(getattr(self.owner, n).data for n in self.names)
+        key = tuple(t.data_ptr() for t in srcs)
+        if key != self._gather_key:
+            self._gather_calls = self._gather_plan(srcs)
+            # holding the sources keeps their addresses from being reused by new tensors
+            self._gather_srcs, self._gather_key = srcs, key
+
     def _gather(self, miss: torch.Tensor, n_miss: torch.Tensor, stream) -> None:
-        """expert_cache_gather of every mirrored tensor over one miss list, six per call."""
+        """expert_cache_gather of every mirrored tensor over one miss list, six per call,
+        with the calls `_plan` resolved."""
         h = lib()
+        tail = (miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, stream)
+        for args in self._gather_calls:
+            rc = h.expert_cache_gather(*args, *tail)
+            if rc != 0:
+                raise RuntimeError(f"expert_cache_gather failed rc={rc}")
+
+    def _gather_plan(self, srcs) -> tuple:
+        """The (dst, src, bytes) x 6 argument lists of the gather calls, padded with a
+        repeat (the library copies a repeated buffer once)."""
         dsts = [self.slots[n] for n in self.names]
-        srcs = [getattr(self.owner, n).data for n in self.names]
+        calls = []
         for i in range(0, len(dsts), GATHER_SLOTS):
-            gd, gs = dsts[i:i + GATHER_SLOTS], srcs[i:i + GATHER_SLOTS]
-            while len(gd) < GATHER_SLOTS:  # pad with a repeat; the library copies it once
+            gd, gs = dsts[i:i + GATHER_SLOTS], list(srcs[i:i + GATHER_SLOTS])
+            while len(gd) < GATHER_SLOTS:
                 gd.append(gd[-1])
                 gs.append(gs[-1])
             args = []
             for d, s in zip(gd, gs):
-                args += [_ptr(d), ctypes.c_void_p(device_address(s)),
-                         ctypes.c_long(_bytes_per_expert(s))]
-            rc = h.expert_cache_gather(*args, _ptr(miss), _ptr(n_miss), self.chunks,
-                                       self.lanes, stream)
-            if rc != 0:
-                raise RuntimeError(f"expert_cache_gather failed rc={rc}")
+                args += [d.data_ptr(), device_address(s), _bytes_per_expert(s)]
+            calls.append(tuple(args))
+        return tuple(calls)
