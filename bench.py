@@ -574,8 +574,8 @@ def _row(t, l):
 
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
                  W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
-                 configs=((None, 0, False), (1.0, 1, False), (1.0, 1, True), (0.8, 1, True),
-                          (1.0, 2, True))):
+                 configs=((None, 0, False, None), (1.0, 1, False, None), (1.0, 1, True, None),
+                          (0.8, 1, True, None), (0.8, 1, True, 1), (1.0, 2, True, None))):
     """Prefetch over a window of the timed steps, every run from the same start state, as
     one captured graph per decode step. With a lookahead of d layers:
       d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
@@ -588,7 +588,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     CU (C = 0: no compute, so prefetch has nothing to hide behind). The predictor is the true
     routing with each id replaced, with probability 1 - accuracy, by a random expert;
     accuracy 1.0 is an upper bound no real predictor reaches. `configs` lists (accuracy,
-    lookahead, one launch) triples; (None, 0, False) is the run without prefetch."""
+    lookahead, one launch, insert budget per prefetch step or None for S); (None, 0, False,
+    None) is the run without prefetch."""
     K = min(window, T - W)
     i32 = torch.int32
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
@@ -629,9 +630,10 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
 
-    def launch(cur, la, one, spin):
+    def launch(cur, la, one, budget, spin):
         c = ctypes.c_void_p(cur.cuda_stream)
         sd = ctypes.c_void_p(side.cuda_stream)
+        pa = [a[:4] + (budget,) + a[5:] for a in p_args]
 
         def copy(l):
             side.wait_stream(cur)
@@ -641,15 +643,15 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
 
         rc = 0
         for j in range(min(la, L)):
-            rc |= lib.expert_cache_prefetch(*p_args[j], c) | copy(j)
+            rc |= lib.expert_cache_prefetch(*pa[j], c) | copy(j)
         for l in range(L):
             n = l + la
             if la and n < L and one:
                 rc |= lib.expert_cache_manage_remap_prefetch(*m_args[l], _row(pred_static, n),
-                                                             mk, S, *p_args[n][5:], c)
+                                                             mk, budget, *pa[n][5:], c)
                 rc |= copy(n)
             elif la and n < L:
-                rc |= lib.expert_cache_prefetch(*p_args[n], c) | copy(n)
+                rc |= lib.expert_cache_prefetch(*pa[n], c) | copy(n)
                 rc |= lib.expert_cache_manage_remap(*m_args[l], c)
             else:
                 rc |= lib.expert_cache_manage_remap(*m_args[l], c)
@@ -664,7 +666,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     out = []
     base_ms = {}
     for C in compute:
-        for q, la, one in configs:
+        for q, la, one, budget in configs:
+            budget = S if budget is None else budget
             if q is None:
                 pred = None
             else:
@@ -680,7 +683,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream(), la, one, int(C * cyc_per_us))
+                launch(torch.cuda.current_stream(), la, one, budget, int(C * cyc_per_us))
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             a.record()
@@ -711,6 +714,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             gbps = moved * B_exp / elapsed / 1e9
             out.append({"compute_us_per_layer": C, "predictor_accuracy": q,
                         "lookahead_layers": la, "one_launch": one,
+                        "insert_budget": budget if q is not None else None,
                         "ms_per_step": round(ms, 4),
                         "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
                         "moved_GBps": round(gbps, 3),
@@ -718,9 +722,10 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                         "prefetch_inserts": int(pn.sum()), "prefetch_used": used,
                         "critical_path_inserts": int(nm.sum()),
                         "real_step_hit_rate": round(1.0 - float(nm.sum()) / distinct, 5)})
+            capped = f", budget {budget}" if q is not None and budget < S else ""
             log(f"prefetch leg, compute {C} us/layer, predictor "
                 f"{'none' if q is None else q}, lookahead {la}"
-                f"{', one launch' if one else ''}: {ms:.3f} ms/step "
+                f"{', one launch' if one else ''}{capped}: {ms:.3f} ms/step "
                 f"({base_ms[C] / ms:.3f}x), {moved} experts moved at {gbps:.2f} GB/s, "
                 f"{int(pn.sum())} prefetched ({used} used), {int(nm.sum())} on the critical "
                 f"path")
