@@ -27,6 +27,10 @@ Printed (one JSON line on stdout):
                50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
                routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one
                and two layers ahead
+  fused        expert_cache_fused (the LRU step plus both moe_align_block_size outputs,
+               block size 16) per layer-step in graph replay, 8 layers x 256 steps of three
+               workloads from a cold start; cpu_baseline.fused_us_per_layer_step times the
+               oracle's fused step on the same steps
 
     python bench.py [--steps K] [--warmup W] [--slots 64] [--policy lfu]
 """
@@ -50,6 +54,9 @@ WORKLOAD = "48-layer-e128"
 TARGET_SLOTS = {"single-layer-e128": 64, "48-layer-e128": 64, "48-layer-e128-batch4": 48,
                 "8-layer-e8-bf16": 4, "8-layer-e256-fp8": 128}
 MAX_STEPS = {"8-layer-e256-fp8": 64}
+# expert_cache_fused leg: (workload, slots), and its shape
+FUSED_CASES = (("48-layer-e128", 64), ("48-layer-e128-batch4", 48), ("8-layer-e256-fp8", 128))
+FUSED_LAYERS, FUSED_STEPS, FUSED_BS = 8, 256, 16
 
 
 def log(*a):
@@ -80,6 +87,8 @@ def parse():
     p.add_argument("--lanes", type=int, default=None)
     p.add_argument("--no-prefetch", action="store_true",
                    help="skip the next-layer prefetch leg")
+    p.add_argument("--no-fused", action="store_true",
+                   help="skip the expert_cache_fused leg")
     p.add_argument("--traffic-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: 16 gathers of one expert each and 8 plain "
                         "device copies of 64 MiB (the counter calibration), nothing else")
@@ -427,6 +436,8 @@ def main():
         prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[W], L, E, S,
                                 mk, policy, decay, W, T, B_exp, chunks, lanes, dev, peak)
 
+    fused = None if args.no_fused else fused_leg(torch, np, lib, dev)
+
     sweep = None
     if not args.no_hit_sweep:
         sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
@@ -488,6 +499,7 @@ def main():
                                  "kernel on one 256 MB slab)"},
         "cpu_baseline": cpu,
         "prefetch": prefetch,
+        "fused": fused,
         "hit_rate_sweep": sweep,
     }
     print(json.dumps(res), flush=True)
@@ -565,7 +577,136 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
             "policy_us_per_layer_step_threads": round(policy_par_us, 4),
             "policy_threads": threads,
             "host_memcpy_GBps": round(host_memcpy, 2),
+            "fused_us_per_layer_step": None if args.no_fused else _cpu_fused(np, oracle),
+            "pcie_round_trip_us_per_layer_step": _pcie_round_trip(torch),
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _pcie_round_trip(torch, n=2000):
+    """What a CPU policy path adds per layer-step on top of its own compute: the step's
+    routing ids (128 int32) copied to the host and synchronized on, and its outputs (the
+    slot ids plus a small miss list, 1 KB) copied back."""
+    dev = torch.device("cuda:0")
+    ids_d = torch.zeros(128, dtype=torch.int32, device=dev)
+    ids_h = torch.empty(128, dtype=torch.int32, pin_memory=True)
+    out_h = torch.zeros(256, dtype=torch.int32, pin_memory=True)
+    out_d = torch.empty(256, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ids_h.copy_(ids_d, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        out_d.copy_(out_h, non_blocking=True)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / n * 1e6
+    log(f"cpu baseline: PCIe round trip of one layer-step's ids and outputs {us:.2f} us")
+    return round(us, 3)
+
+
+def _align_lengths(mk, E, bs):
+    """vLLM's moe_align_block_size buffer lengths (kernels/expert_cache.hip:606-609)."""
+    L = min(mk * bs, mk + E * (bs - 1)) if mk < E else mk + E * (bs - 1)
+    return L, -(-L // bs)
+
+
+def _fused_routing(np, name):
+    from vllm_expert_cache import traces
+    w = traces.WORKLOADS[name]
+    return w, np.stack([traces.routing(w, l, FUSED_STEPS) for l in range(FUSED_LAYERS)],
+                       axis=1)  # [T, layers, mk]
+
+
+def _cpu_fused(np, oracle):
+    """The oracle's fused step (one core) over the fused leg's steps, us per layer-step."""
+    out = {}
+    for name, S in FUSED_CASES:
+        w, ids = _fused_routing(np, name)
+        E, mk = w.experts, w.mk
+        L, NB = _align_lengths(mk, E, FUSED_BS)
+        states = [oracle.State(E, S) for _ in range(FUSED_LAYERS)]
+        rows = [np.ascontiguousarray(ids[:, l]) for l in range(FUSED_LAYERS)]
+        t0 = oracle.now()
+        for l in range(FUSED_LAYERS):
+            assert states[l].fused_trace(rows[l], FUSED_BS, L, NB) == 0
+        out[name] = round((oracle.now() - t0) / (FUSED_STEPS * FUSED_LAYERS) * 1e6, 3)
+    log(f"cpu baseline, fused: {out} us/layer-step (one core)")
+    return out
+
+
+def fused_leg(torch, np, lib, dev):
+    """expert_cache_fused per layer-step: FUSED_LAYERS launches captured in one graph,
+    replayed for FUSED_STEPS steps of each FUSED_CASES workload from a cold start, the
+    step's ids copied into the graph's input first. The kernel is latency-bound; its
+    algorithmic bytes per call are the policy step's (ids, state read and written, the
+    miss list) plus both align outputs written."""
+    keys = ("sorted_hot", "eids_hot", "npad_hot", "sorted_cold", "eids_cold", "npad_cold")
+    runs = []
+    for name, S in FUSED_CASES:
+        w, ids_np = _fused_routing(np, name)
+        E, mk, Ly = w.experts, w.mk, FUSED_LAYERS
+        L, NB = _align_lengths(mk, E, FUSED_BS)
+        sizes = dict(sorted_hot=L, eids_hot=NB, npad_hot=1, sorted_cold=L, eids_cold=NB,
+                     npad_cold=1)
+        ids_dev = torch.as_tensor(ids_np, device=dev)
+        st = Layers(torch, Ly, E, S, dev)
+        ids_static = torch.zeros((Ly, mk), dtype=torch.int32, device=dev)
+        nm = torch.zeros((Ly,), dtype=torch.int32, device=dev)
+        nm_hist = torch.zeros((FUSED_STEPS, Ly), dtype=torch.int32, device=dev)
+        outs = {k: torch.zeros((Ly, n), dtype=torch.int32, device=dev) for k, n in sizes.items()}
+        args = [(_row(ids_static, l), mk, E, S, min(E, mk), S, st.row("table", l),
+                 st.row("map_cold", l), st.row("slot_expert", l), st.row("slot_stamp", l),
+                 st.row("routed", l), st.row("step", l), st.row("miss", l),
+                 _row(nm, l), FUSED_BS, L, NB, *[_row(outs[k], l) for k in keys])
+                for l in range(Ly)]
+
+        def launch(stream):
+            c = ctypes.c_void_p(stream.cuda_stream)
+            for a in args:
+                if lib.expert_cache_fused(*a, c):
+                    raise RuntimeError("expert_cache_fused launch failed")
+
+        snap = st.snapshot()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            launch(side)  # warm-up outside capture
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        st.restore(snap)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            launch(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        for t in range(FUSED_STEPS):  # inserts per step, untimed
+            ids_static.copy_(ids_dev[t], non_blocking=True)
+            g.replay()
+            nm_hist[t].copy_(nm, non_blocking=True)
+        st.restore(snap)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for t in range(FUSED_STEPS):
+            ids_static.copy_(ids_dev[t], non_blocking=True)
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        del g
+        us = a.elapsed_time(b) * 1e3 / (FUSED_STEPS * Ly)
+        inserts = float(nm_hist.float().mean())
+        policy_bytes = 4 * mk + 2 * (8 * E + 12 * S + 8) + 8 * inserts + 4
+        out_bytes = 2 * (4 * L + 4 * NB + 4)
+        runs.append({"workload": name, "experts": E, "slots": S, "ids_per_step": mk,
+                     "block_size": FUSED_BS, "graph_us_per_layer_step": round(us, 3),
+                     "algorithmic_bytes_per_call": int(policy_bytes + out_bytes),
+                     "achieved_GBps": round((policy_bytes + out_bytes) / (us * 1e3), 3),
+                     "inserts_per_layer_step": round(inserts, 4)})
+        log(f"fused {name}: E={E} S={S} mk={mk} bs={FUSED_BS}, {us:.2f} us/layer-step in "
+            f"graph replay, {int(policy_bytes + out_bytes)} algorithmic bytes per call")
+    return {"bound": "latency (one wave, dependent LDS phases)", "layers": FUSED_LAYERS,
+            "steps": FUSED_STEPS, "def": "graph replay of one launch per layer, including "
+            "the per-step id copy; LRU, cold start. cpu_baseline.fused_us_per_layer_step is "
+            "the oracle's fused step in C on one core with the state in host memory: it "
+            "leaves out moving each step's ids to the host and the outputs back, which a "
+            "CPU path would pay every layer-step", "runs": runs}
 
 
 def _row(t, l):

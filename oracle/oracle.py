@@ -51,6 +51,8 @@ def lib():
         h.oracle_fused.restype = _I
         h.oracle_fused.argtypes = ([_P, _I, _I, _I, _I, _I] + [_P] * 8 + [_I, _I, _I]
                                    + [_P] * 6)
+        h.oracle_fused_trace.restype = _I
+        h.oracle_fused_trace.argtypes = [_P] + [_I] * 7 + [_P] * 14
         _LIB = h
     return _LIB
 
@@ -119,6 +121,18 @@ class State:
             *[_ptr(out[k]) for k in ("sorted_hot", "eids_hot", "npad_hot", "sorted_cold",
                                      "eids_cold", "npad_cold")])
         return rc, out
+
+    def fused_trace(self, ids, bs: int, L: int, NB: int) -> int:
+        """fused over every row of ids[T, mk] (max_distinct = min(E, mk), max_inserts = S) in
+        one C loop; the align outputs are discarded. For timing."""
+        ids = np.ascontiguousarray(np.asarray(ids).astype(np.int32))
+        T, mk = ids.shape
+        out = [np.zeros(n, np.int32) for n in (L, NB, 1, L, NB, 1)]
+        return lib().oracle_fused_trace(
+            _ptr(ids), T, mk, self.E, self.S, int(bs), int(L), int(NB), _ptr(self.table),
+            _ptr(self.map_cold), _ptr(self.slot_expert), _ptr(self.slot_stamp),
+            _ptr(self.routed), _ptr(self.step), _ptr(self.miss), _ptr(self.n_miss),
+            *[_ptr(o) for o in out])
 
     def misses(self):
         n = int(self.n_miss[0])

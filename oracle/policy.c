@@ -444,3 +444,26 @@ int oracle_fused(const int32_t* ids, int mk, int E, int S, int max_distinct, int
   free(kc);
   return 0;
 }
+
+/*
+ * oracle_fused over a whole routing trace ids[T * mk] of one layer, with max_distinct =
+ * min(E, mk) and max_inserts = S, for the CPU-baseline timing in bench.py. The align
+ * outputs hold the last step's. Returns 0, or the first failing step's return code.
+ */
+int oracle_fused_trace(const int32_t* ids, int T, int mk, int E, int S, int bs, int L, int NB,
+                       int32_t* table, int32_t* map_cold, int32_t* slot_expert,
+                       int64_t* slot_stamp, uint8_t* routed, int64_t* step, int32_t* miss,
+                       int32_t* n_miss, int32_t* sorted_hot, int32_t* eids_hot,
+                       int32_t* npad_hot, int32_t* sorted_cold, int32_t* eids_cold,
+                       int32_t* npad_cold) {
+  if (T < 0 || mk < 0) return -1;
+  const int md = mk < E ? mk : E;
+  for (int t = 0; t < T; t++) {
+    const int rc = oracle_fused(ids + (size_t)t * (size_t)mk, mk, E, S, md, S, table, map_cold,
+                                slot_expert, slot_stamp, routed, step, miss, n_miss, bs, L, NB,
+                                sorted_hot, eids_hot, npad_hot, sorted_cold, eids_cold,
+                                npad_cold);
+    if (rc != 0) return rc;
+  }
+  return 0;
+}

@@ -336,3 +336,22 @@ def test_serial_equals_rank_on_random_shapes(seed):
         for f in State.FIELDS:
             assert np.array_equal(getattr(a, f), getattr(b, f)), (seed, t, f)
         _check_invariants(b)
+
+
+def test_fused_trace_is_the_stepwise_fused():
+    """oracle_fused_trace (bench.py's CPU timing loop) leaves the state that calling the
+    fused step once per row leaves."""
+    from vllm_expert_cache import traces
+
+    w = traces.WORKLOADS["48-layer-e128-batch4"]
+    ids = traces.routing(w, 2, steps=60)
+    E, S, bs = 128, 48, 16
+    mk = ids.shape[1]
+    L, NB = align_lengths(mk, E, bs)
+    a, b = State(E, S), State(E, S)
+    for row in ids:
+        rc, _ = a.fused(row, min(E, mk), S, bs, L, NB)
+        assert rc == 0
+    assert b.fused_trace(ids, bs, L, NB) == 0
+    for f in ("table", "map_cold", "slot_expert", "slot_stamp", "step", "miss", "n_miss"):
+        assert np.array_equal(getattr(a, f), getattr(b, f)), f
