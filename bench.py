@@ -22,11 +22,13 @@ Printed (one JSON line on stdout):
                core deciding the misses, and one hipMemcpyAsync per (miss, buffer), on a
                sample of the same steps
   prefetch     a window of the timed steps with and without next-layer prefetch (each
-               layer's predicted experts installed by expert_cache_prefetch and copied on a
+               layer's predicted experts installed by the prefetch step and copied on a
                side stream during an earlier layer), with no model compute and with a
                50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
                routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one
-               and two layers ahead
+               and two layers ahead, the prefetch step launched on its own
+               (expert_cache_prefetch) or inside the policy launch
+               (expert_cache_manage_remap_prefetch), and an insert budget of one
   fused        expert_cache_fused (the LRU step plus both moe_align_block_size outputs,
                block size 16) per layer-step in graph replay, 8 layers x 256 steps of three
                workloads from a cold start; cpu_baseline.fused_us_per_layer_step times the
