@@ -435,8 +435,12 @@ def main():
 
     prefetch = None
     if not args.no_prefetch:
+        # about 130 GB moved per run at most: 1,024 steps of the default workload, fewer
+        # where experts are hundreds of MB
+        per_step = max(1.0, inserts * B_exp / K)
         prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[W], L, E, S,
-                                mk, policy, decay, W, T, B_exp, chunks, lanes, dev, peak)
+                                mk, policy, decay, W, T, B_exp, chunks, lanes, dev, peak,
+                                window=max(32, min(1024, int(130e9 / per_step))))
 
     fused = None if args.no_fused else fused_leg(torch, np, lib, dev)
 
