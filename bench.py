@@ -91,6 +91,12 @@ def parse():
                    help="skip the next-layer prefetch leg")
     p.add_argument("--no-fused", action="store_true",
                    help="skip the expert_cache_fused leg")
+    p.add_argument("--routes", default=None,
+                   help="replay a recorded trace instead of the synthetic routing: an npz "
+                        "whose ids are [T, L, mk] with -1 padding (the reference's routes.npz "
+                        "format); experts keep the --workload layout")
+    p.add_argument("--experts", type=int, default=None,
+                   help="experts per layer of a --routes trace (default: the workload's)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: 16 gathers of one expert each and 8 plain "
                         "device copies of 64 MiB (the counter calibration), nothing else")
@@ -201,23 +207,39 @@ def main():
     w = traces.WORKLOADS[args.workload]
     L = args.layers or w.layers
     E, mk = w.experts, w.mk
+    steps = w.steps
+    name = w.name
+    recorded = None
+    if args.routes:
+        recorded = traces.load_routes(args.routes)
+        L = min(L if args.layers else recorded.shape[1], recorded.shape[1])
+        recorded = recorded[:, :L]
+        E = args.experts or w.experts
+        if recorded.max() >= E:
+            raise SystemExit(f"{args.routes}: expert id {recorded.max()} >= {E} experts; "
+                             f"pass --experts")
+        mk, steps = recorded.shape[2], recorded.shape[0]
+        name = f"routes:{Path(args.routes).name}"
     S = args.slots or TARGET_SLOTS[w.name]
     if mk > S:
-        raise SystemExit(f"{w.name}: {mk} routing ids per step exceed {S} slots, so every step "
+        raise SystemExit(f"{name}: {mk} routing ids per step exceed {S} slots, so every step "
                          f"reads through and there is nothing to time; pick --slots >= {mk}")
     policy = 1 if args.policy == "lfu" else 0
     decay = 64
     chunks = args.chunks or DEFAULT_CHUNKS
     lanes = args.lanes or DEFAULT_LANES
-    W = min(args.warmup, w.steps - 1)
-    K = args.steps or min(w.steps - W, MAX_STEPS.get(w.name, w.steps))
+    W = min(args.warmup, steps - 1)
+    K = args.steps or min(steps - W, MAX_STEPS.get(name, steps))
     T = W + K
     bufs = [b.nbytes for b in w.buffers]
     B_exp = sum(bufs)
 
     # ---- routing and host expert store --------------------------------------------------
     t0 = time.time()
-    ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)  # [T, L, mk]
+    if recorded is None:
+        ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)  # [T, L, mk]
+    else:
+        ids_np = np.ascontiguousarray(recorded[:T], dtype=np.int32)
     ids_dev = torch.as_tensor(ids_np, device=dev)
     host = []  # host[l][b]: pinned [E * bytes_b]
     host_store = "per layer"
@@ -322,7 +344,7 @@ def main():
     elapsed_s = max(wall, gpu_ms / 1e3)
     nm = nm_hist.cpu().numpy()
     inserts = int(nm[W:T].sum())
-    distinct = sum(len(np.unique(ids_np[t, l])) for t in range(W, T) for l in range(L))
+    distinct = int(_distinct(np, ids_np[W:T]).sum())
     gathered = inserts * B_exp
     value = gathered / elapsed_s / 1e9
     log(f"timed: {K} steps in {elapsed_s:.2f}s ({1e3 * elapsed_s / K:.3f} ms/step), "
@@ -468,9 +490,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8",
-        "data": "synthetic",
-        "config": {"workload": w.name, "layers": L, "experts": E, "top_k": w.top_k,
-                   "tokens_per_step": w.tokens, "slots": S, "policy": args.policy,
+        "data": "synthetic" if recorded is None else "recorded routing, synthetic experts",
+        "config": {"workload": name, "expert_layout": w.name, "layers": L, "experts": E,
+                   "ids_per_step": mk, "top_k": None if recorded is not None else w.top_k,
+                   "tokens_per_step": None if recorded is not None else w.tokens,
+                   "slots": S, "policy": args.policy,
                    "decay": decay, "bytes_per_expert": B_exp, "host_store_GB":
                    round(L * E * B_exp / 1e9, 2), "host_store": host_store,
                    "gather_grid": [chunks, lanes],
@@ -715,6 +739,14 @@ def fused_leg(torch, np, lib, dev):
             "CPU path would pay every layer-step", "runs": runs}
 
 
+def _distinct(np, ids):
+    """Distinct expert ids per [..., mk] row, -1 padding not counted."""
+    srt = np.sort(ids, axis=-1)
+    new = np.ones(srt.shape, bool)
+    new[..., 1:] = srt[..., 1:] != srt[..., :-1]
+    return (new & (srt >= 0)).sum(-1)
+
+
 def _row(t, l):
     return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
 
@@ -742,7 +774,9 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
     routed = np.zeros((K, L, E), bool)
     for i in range(mk):
-        routed[tt, ll, ids_np[W:W + K, :, i]] = True
+        v = ids_np[W:W + K, :, i]
+        m = v >= 0  # -1 pads a recorded trace
+        routed[tt[m], ll[m], v[m]] = True
     distinct = int(routed.sum())
 
     # spin cycles per microsecond, measured
@@ -821,7 +855,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 rng = np.random.default_rng(int(q * 1000))
                 pred = ids_np[W:W + K].copy()
                 if q < 1.0:
-                    wrong = rng.random(pred.shape) >= q
+                    wrong = (rng.random(pred.shape) >= q) & (pred >= 0)
                     pred[wrong] = rng.integers(0, E, int(wrong.sum()))
                 pred_dev = torch.as_tensor(pred, device=dev)
             st.restore(snap)
@@ -886,8 +920,7 @@ def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
     hit rate and gather volume depend only on the policy). Also the graph's time per layer,
     which is kernel time plus graph node gaps plus the per-step id copy."""
     T = ids_np.shape[0]
-    srt = np.sort(ids_np, axis=-1)
-    distinct = 1 + (np.diff(srt, axis=-1) != 0).sum(-1)  # [T, L]
+    distinct = _distinct(np, ids_np)  # [T, L]
     out = []
     for S in w.slots:
         if mk > S:

@@ -147,6 +147,78 @@ def test_reference_policy_suites(suite, policy, lib_name):
     assert np.array_equal(got["final"].routed[0].cpu().numpy(), want["final"].routed)
 
 
+def _recorded_trace(path) -> np.ndarray:
+    """A trace in the replay format (npz "ids" [T, L, mk], -1 padding): the file TRACE names
+    if it exists, else one written here through save_routes -- 400 steps x 8 layers of 1 to
+    5 tokens x top-10 over 512 experts (Zipf 1.1 with 0.6 per-expert repeat), padded to 50
+    ids -- and read back through load_routes."""
+    import os
+    tr = os.environ.get("TRACE", "routes.npz")
+    if os.path.exists(tr):
+        return traces.load_routes(tr)
+    rng = np.random.default_rng(7)
+    E, T, L, K, TOK = 512, 400, 8, 10, 5
+    w = np.arange(1, E + 1, dtype=float) ** -1.1
+    w /= w.sum()
+    ids = np.full((T, L, TOK * K), -1, np.int32)
+    for l in range(L):
+        perm = rng.permutation(E)
+        prev = [perm[rng.choice(E, K, replace=False, p=w)] for _ in range(TOK)]
+        for t in range(T):
+            for j in range(int(rng.integers(1, TOK + 1))):
+                keep = prev[j][rng.random(K) < 0.6]
+                fill = [e for e in perm[rng.choice(E, 3 * K, p=w)] if e not in keep]
+                row = np.concatenate([keep, np.array(fill[:K - len(keep)], np.int64)])
+                ids[t, l, j * K:(j + 1) * K] = row
+                prev[j] = row
+    traces.save_routes(str(path), ids)
+    return traces.load_routes(str(path))
+
+
+@pytest.mark.parametrize("lib_name", ["product", "reference"])
+@pytest.mark.parametrize("policy", [LRU, LFU])
+def test_real_trace_suite(tmp_path, policy, lib_name):
+    """The reference's sixth policy suite (tests/test_policy.py:222-232) on a trace in its
+    replay format: layer TRACE_LAYER (default 7), the first 400 steps, each step's ids with
+    the -1 padding removed (so mk varies per step), E = 512, S = 257, max_distinct = 128,
+    max_inserts = 64, against the oracle after every step."""
+    import os
+    h = gu.lib() if lib_name == "product" else gu.ref_lib()
+    if h is None:
+        pytest.skip("reference library not built")
+    ids_all = _recorded_trace(tmp_path / "routes.npz")
+    layer = int(os.environ.get("TRACE_LAYER", "7"))
+    rows = [ids_all[t, layer][ids_all[t, layer] >= 0].astype(np.int32)
+            for t in range(min(400, ids_all.shape[0]))]
+    E, S, md, mi, decay = 512, 257, 128, 64, 8
+    hot = sorted(np.random.default_rng(1).choice(E, S, replace=False).tolist())
+    st = gu.Layers(1, E, S, miss_cap=mi, hot=hot)
+    T = len(rows)
+    rec = {k: torch.zeros(shape, dtype=torch.int32, device=gu.DEV) for k, shape in (
+        ("n_miss", (T, 1)), ("miss", (T, 1, 2 * mi)),
+        ("state", (T, 1, oracle.state_words(E, S))))}
+    d_rows = [torch.as_tensor(r, device=gu.DEV) for r in rows]
+    for t, r in enumerate(d_rows):
+        assert gu.manage_call(h, st, 0, gu.ptr(r) if r.numel() else None, r.numel(), md, mi,
+                              policy, decay) == 0
+        rec["n_miss"][t].copy_(st.n_miss[:, 0])
+        rec["miss"][t].copy_(st.miss)
+        rec["state"][t].copy_(st.state_words())
+    torch.cuda.synchronize()
+    got = {k: v.cpu().numpy() for k, v in rec.items()}
+    ref = oracle.State(E, S, hot, miss_cap=mi)
+    want = {k: np.zeros_like(v) for k, v in got.items()}
+    for t, r in enumerate(rows):
+        assert ref.manage(r, md, mi, policy, decay) == 0
+        want["n_miss"][t, 0] = ref.n_miss[0]
+        want["miss"][t, 0] = ref.miss
+        want["state"][t, 0] = np.concatenate([ref.table, ref.map_cold, ref.slot_expert,
+                                              ref.slot_stamp.view(np.int32),
+                                              ref.step.view(np.int32)])
+    _assert_same(got, want, ("n_miss", "miss", "state"), f"{lib_name}:real-trace-L{layer}")
+    assert int(want["n_miss"].sum()) > 0
+
+
 REF_CASES = [("48-layer-e128", 16, "lfu"), ("48-layer-e128", 64, "lfu"),
              ("48-layer-e128", 64, "lru"), ("48-layer-e128-batch4", 32, "lfu"),
              ("8-layer-e256-fp8", 128, "lru")]

@@ -77,3 +77,20 @@ def test_routes_npz_round_trip(tmp_path):
     traces.save_routes(str(p), ids)
     back = traces.load_routes(str(p))
     assert back.shape == (20, 3, 8) and np.array_equal(back, ids)
+
+
+def test_bench_counts_distinct_experts_without_padding():
+    """bench.py's hit rate divides by the distinct routed experts of each (step, layer); on a
+    recorded trace the -1 padding is not an expert."""
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+
+    ids = np.array([[[3, 3, -1, 5], [-1, -1, -1, -1]], [[1, 2, 3, 4], [0, 0, 0, 0]]], np.int32)
+    assert bench._distinct(np, ids).tolist() == [[2, 0], [4, 1]]
+    rng = np.random.default_rng(0)
+    big = rng.integers(-1, 40, size=(50, 3, 12)).astype(np.int32)
+    want = [[len(set(r[r >= 0].tolist())) for r in step] for step in big]
+    assert bench._distinct(np, big).tolist() == want
