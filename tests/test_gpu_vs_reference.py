@@ -41,7 +41,9 @@ REF_SIZES = (819200, 409600, 51200, 640, 25600, 2560)   # tests/test_policy.py:2
 
 
 SPEED_ASSERT = os.environ.get("EC_SPEED_ASSERT", "1") != "0"
-MARGIN = 1.05
+# a regression guard, not the measurement (the timings are printed): the closest case, the
+# 44 MB experts where both sides run at the link's rate, is a tie, so leave room for noise
+MARGIN = 1.10
 
 
 def _not_slower(this: float, reference: float) -> bool:
