@@ -16,7 +16,7 @@ captured in HIP graphs so that host launch cost is out of the picture:
     (4 layers, 128 slots, 128 ids per step).
 
 Each test prints one "speed:" line per figure (run pytest with -s to see them) and asserts
-this library is not slower than the reference beyond a 5 % noise margin. EC_SPEED_ASSERT=0
+this library is not slower than the reference beyond a 10 % noise margin. EC_SPEED_ASSERT=0
 keeps only the byte checks (for runs under a profiler, whose per-dispatch cost swamps
 kernels of a few microseconds).
 """
