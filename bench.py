@@ -25,8 +25,8 @@ Printed (one JSON line on stdout):
                layer's predicted experts installed by the prefetch step and copied on a
                side stream during an earlier layer), with no model compute and with a
                50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
-               routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one
-               and two layers ahead, the prefetch step launched on its own
+               routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one,
+               two and four layers ahead, the prefetch step launched on its own
                (expert_cache_prefetch) or inside the policy launch
                (expert_cache_manage_remap_prefetch), and an insert budget of one
   fused        expert_cache_fused (the LRU step plus both moe_align_block_size outputs,
@@ -754,7 +754,8 @@ def _row(t, l):
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
                  W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
                  configs=((None, 0, False, None), (1.0, 1, False, None), (1.0, 1, True, None),
-                          (0.8, 1, True, None), (0.8, 1, True, 1), (1.0, 2, True, None))):
+                          (0.8, 1, True, None), (0.8, 1, True, 1), (1.0, 2, True, None),
+                          (1.0, 4, True, None))):
     """Prefetch over a window of the timed steps, every run from the same start state, as
     one captured graph per decode step. With a lookahead of d layers:
       d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
