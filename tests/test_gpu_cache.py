@@ -148,3 +148,49 @@ def test_refresh_follows_a_source_that_moves():
     torch.cuda.synchronize()
     for f, t in before.items():  # refused before the policy step ran
         assert torch.equal(getattr(cache, f), t), f
+
+
+class WideOwner(torch.nn.Module):
+    """Eight per-expert tensors in pinned host memory (weights, scales, zero points and
+    biases of odd widths), more than one gather call's six buffers."""
+
+    SHAPES = {"w13_weight": ((E, 96, 64), torch.int8), "w2_weight": ((E, 64, 48), torch.int8),
+              "w13_weight_scale": ((E, 96, 1), torch.float32),
+              "w2_weight_scale": ((E, 64, 1), torch.float32),
+              "w13_weight_zero": ((E, 96, 4), torch.int8), "w2_weight_zero": ((E, 64, 4), torch.int8),
+              "w13_bias": ((E, 96), torch.float32), "w2_bias": ((E, 64), torch.bfloat16)}
+
+    def __init__(self, seed):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        for n, (shape, dtype) in self.SHAPES.items():
+            t = torch.empty(shape, dtype=dtype, pin_memory=True)
+            t.view(torch.uint8).copy_(torch.randint(0, 256, t.view(torch.uint8).shape,
+                                                    dtype=torch.uint8, generator=g))
+            setattr(self, n, t)
+
+
+def test_refresh_with_more_tensors_than_one_gather_takes():
+    """Eight mirrored tensors take two gather calls per refresh (six buffers each, the second
+    padded with repeats). After every step, eagerly and with a prefetch along the refresh,
+    every resident slot of every tensor holds its expert's bytes."""
+    names = list(WideOwner.SHAPES)
+    owners = [WideOwner(1), WideOwner(2)]
+    caches = [ExpertSlotCache(o, names, E, S, gu.DEV) for o in owners]
+    assert all(len(c.names) == 8 for c in caches)
+    rng = np.random.default_rng(8)
+    for t in range(30):
+        ids = [torch.as_tensor(np.stack([rng.choice(E, K, replace=False) for _ in range(2)])
+                               .astype(np.int32), device=gu.DEV) for _ in range(2)]
+        pred = torch.as_tensor(rng.choice(E, K, replace=False).astype(np.int32), device=gu.DEV)
+        if t % 2:
+            caches[1].prefetch(pred, along=caches[0])
+        caches[0].refresh(ids[0])
+        caches[1].refresh(ids[1])
+        torch.cuda.synchronize()
+        for c, o in zip(caches, owners):
+            live = torch.nonzero(c.slot_expert >= 0).flatten()
+            experts = c.slot_expert[live].long().cpu()
+            for n in names:  # bytes: random bits read as floats include NaNs
+                want = getattr(o, n)[experts].view(torch.uint8)
+                assert torch.equal(c.slots[n][live].cpu().view(torch.uint8), want), (t, n)
