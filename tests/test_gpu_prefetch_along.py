@@ -178,11 +178,13 @@ def _pair(seed):
     return owners, caches
 
 
-def test_cache_along_equals_separate_launches():
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_cache_along_equals_separate_launches(dtype):
     """Two-layer decode: layer 1's prefetch staged along layer 0's refresh, and layer 0's
     next-step prefetch staged on layer 1, against the same prefetches launched on their
     own. Some steps also restage (the first staged step then runs alone) or read layer 0
-    through (join launches what is staged on it and what it has staged elsewhere)."""
+    through (join launches what is staged on it and what it has staged elsewhere). Routing
+    ids and predictions come as int32 or int64, as vLLM may hand either."""
     owners, along = _pair(11)
     _, alone = _pair(11)
     srcs = [_sources(o) for o in owners]
@@ -193,11 +195,12 @@ def test_cache_along_equals_separate_launches():
         ids0 = nxt0
         ids1 = rng.choice(E, K, replace=False).astype(np.int32)
         nxt0 = rng.choice(E, K, replace=False).astype(np.int32)
-        p1 = torch.as_tensor(_predict(ids1, E, 0.75, rng), device=gu.DEV)
-        p1b = torch.as_tensor(rng.choice(E, 4, replace=False).astype(np.int32), device=gu.DEV)
-        p0 = torch.as_tensor(_predict(nxt0, E, 0.75, rng), device=gu.DEV)
-        d0 = torch.as_tensor(ids0, device=gu.DEV)
-        d1 = torch.as_tensor(ids1, device=gu.DEV)
+        p1 = torch.as_tensor(_predict(ids1, E, 0.75, rng), device=gu.DEV).to(dtype)
+        p1b = torch.as_tensor(rng.choice(E, 4, replace=False).astype(np.int32),
+                              device=gu.DEV).to(dtype)
+        p0 = torch.as_tensor(_predict(nxt0, E, 0.75, rng), device=gu.DEV).to(dtype)
+        d0 = torch.as_tensor(ids0, device=gu.DEV).to(dtype)
+        d1 = torch.as_tensor(ids1, device=gu.DEV).to(dtype)
         mode = t % 4
         # with along=
         if mode == 1:  # restaged: the first prediction runs alone, the second rides
