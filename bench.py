@@ -9,21 +9,35 @@ all 48 layers: per layer, the fused policy step + remap kernel and the gather ke
 plugin launches them, captured once into a HIP graph and replayed per step (the way vLLM
 runs decode). Routing ids for the step are copied into the graph's input buffer first.
 
-Printed (one JSON line on stdout):
+Windows of the trace (4096 steps for this workload):
+  timed        steps W..W+K (--warmup W, --steps K): `value`, `ms_per_step` and `roofline`
+  trace pass   the same graph replayed on to the end of the trace, steps W..4096, and then
+               verified: every resident slot's bytes against the position-hash content of
+               its expert (the host store holds a hash of (layer, expert, buffer, word) in
+               every 4-byte word), and, in the cpu_baseline leg, every layer's per-step
+               n_miss and miss list and final state against the oracle's C policy step
+  steady state the second half of the trace pass (steps 2048..4096)
+
+Printed (one JSON line on stdout; the run exits 1 if any verification fails):
   value        gathered bytes / wall time of the timed steps (GB/s), sources in host memory
+  verified     the checks above, with what each covered
+  trace_pass   whole-job GB/s, ms/step and hit rate over steps W..4096
   roofline     the gather kernel: achieved host->HBM GB/s (algorithmic bytes / kernel time,
-               HIP events on the launch stream over a window of the timed steps) against
-               the measured host->device link peak
+               HIP events on the launch stream over segments of the timed steps) against
+               the measured host->device link peak; roofline.steady_state is the same over
+               segments of the steady-state window
   manage_remap_us_per_layer   cost of the fused policy+remap kernel per layer inside the
                decode graph (hit-rate pass at this budget and policy, whole trace); the
                event-bracketed figure, an upper bound, is manage_remap_us_per_layer_events
   hit_rate     1 - inserts / distinct routed experts over the timed steps
+  hit_rate_sweep  every slot budget x LFU/LRU over the whole trace from a cold start, with
+               the per-layer range
   cpu_baseline the CPU path on this box's host: the policy restated in C (oracle/) on one
-               core deciding the misses, and one hipMemcpyAsync per (miss, buffer), on a
-               sample of the same steps
-  prefetch     a window of the timed steps with and without next-layer prefetch (each
-               layer's predicted experts installed by the prefetch step and copied on a
-               side stream during an earlier layer), with no model compute and with a
+               core over the trace pass, and a CPU-driven cache (that policy deciding the
+               misses, one hipMemcpyAsync per (miss, buffer)) on a sample of the timed steps
+  prefetch     1,024 steps of the steady-state window with and without next-layer prefetch
+               (each layer's predicted experts installed by the prefetch step and copied on
+               a side stream during an earlier layer), with no model compute and with a
                50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
                routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one,
                two and four layers ahead, the prefetch step launched on its own
@@ -56,6 +70,8 @@ WORKLOAD = "48-layer-e128"
 TARGET_SLOTS = {"single-layer-e128": 64, "48-layer-e128": 64, "48-layer-e128-batch4": 48,
                 "8-layer-e8-bf16": 4, "8-layer-e256-fp8": 128}
 MAX_STEPS = {"8-layer-e256-fp8": 64}
+# steps of the verified trace pass where one step moves gigabytes (default: the whole trace)
+TRACE_STEPS = {"8-layer-e256-fp8": 128}
 # expert_cache_fused leg: (workload, slots), and its shape
 FUSED_CASES = (("48-layer-e128", 64), ("48-layer-e128-batch4", 48), ("8-layer-e256-fp8", 128))
 FUSED_LAYERS, FUSED_STEPS, FUSED_BS = 8, 256, 16
@@ -78,6 +94,9 @@ def parse():
                    help="slot budget (default: the workload's target budget)")
     p.add_argument("--policy", choices=("lfu", "lru"), default="lfu")
     p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--no-trace-pass", action="store_true",
+                   help="stop after the timed steps instead of replaying the rest of the "
+                        "trace (the verification then covers steps 0..warmup+steps)")
     p.add_argument("--no-hit-sweep", action="store_true",
                    help="skip the per-budget, per-policy hit-rate pass over the whole trace")
     p.add_argument("--timing-segments", type=int, default=8,
@@ -231,17 +250,24 @@ def main():
     W = min(args.warmup, steps - 1)
     K = args.steps or min(steps - W, MAX_STEPS.get(name, steps))
     T = W + K
+    if T > steps:
+        raise SystemExit(f"{name}: warm-up {W} + timed {K} steps exceed the trace's {steps}")
+    # the trace pass replays the trace from step 0 to TP (the timed steps included) and is
+    # verified at its end; TP is the whole trace unless one step moves gigabytes
+    TP = T if args.no_trace_pass else max(T, min(steps, TRACE_STEPS.get(name, steps)))
+    late0 = TP // 2  # the steady-state window: the second half of the trace pass
     bufs = [b.nbytes for b in w.buffers]
     B_exp = sum(bufs)
 
-    # ---- routing and host expert store --------------------------------------------------
+    # ---- routing, and the host expert store filled with position-hash content ------------
     t0 = time.time()
     if recorded is None:
-        ids_np = np.stack([traces.routing(w, l, T) for l in range(L)], axis=1)  # [T, L, mk]
+        ids_np = np.stack([traces.routing(w, l, steps) for l in range(L)], axis=1)  # [T, L, mk]
     else:
-        ids_np = np.ascontiguousarray(recorded[:T], dtype=np.int32)
+        ids_np = np.ascontiguousarray(recorded, dtype=np.int32)
     ids_dev = torch.as_tensor(ids_np, device=dev)
     host = []  # host[l][b]: pinned [E * bytes_b]
+    content = list(range(L))  # content[l]: the layer whose synthetic experts host[l] holds
     host_store = "per layer"
     try:
         for l in range(L):
@@ -258,17 +284,25 @@ def main():
         torch.cuda.empty_cache()
         shared = [torch.empty(E * b, dtype=torch.uint8, pin_memory=True) for b in bufs]
         host = [shared] * L
+        content = [0] * L
         host_store = f"shared by all layers (pinning {L * E * B_exp / 1e9:.1f} GB failed)"
+    t1 = time.time()
+    for l in sorted(set(content)):
+        for b, nb in enumerate(bufs):
+            traces.fill_expert_store(host[l][b], l, b, nb, E, dev)
+    torch.cuda.synchronize()
     slots = [[torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
              for _ in range(L)]
-    log(f"setup: routing {ids_np.shape}, host store {L * E * B_exp / 1e9:.1f} GB pinned, "
-        f"slots {L * S * B_exp / 1e9:.1f} GB, {time.time() - t0:.1f}s")
+    log(f"setup: routing {ids_np.shape}, host store {L * E * B_exp / 1e9:.1f} GB pinned "
+        f"(position-hash content written in {time.time() - t1:.1f}s), slots "
+        f"{L * S * B_exp / 1e9:.1f} GB, {time.time() - t0:.1f}s")
 
     st = Layers(torch, L, E, S, dev)
     ids_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
     out_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
     nm_static = torch.zeros((L,), dtype=torch.int32, device=dev)
-    nm_hist = torch.zeros((T, L), dtype=torch.int32, device=dev)
+    nm_hist = torch.zeros((TP, L), dtype=torch.int32, device=dev)
+    miss_hist = torch.zeros((TP, L, 2 * S), dtype=torch.int32, device=dev)
 
     def row(t, l):
         return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
@@ -314,91 +348,143 @@ def main():
         launch_step(torch.cuda.current_stream())
     torch.cuda.synchronize()
 
-    def run_steps(t_from, t_to, snaps=None):
+    def run_steps(t_from, t_to, snaps):
         for t in range(t_from, t_to):
-            if snaps is not None and t in snaps:
+            if t in snaps:
                 for f in st.fields:
                     snaps[t][f].copy_(getattr(st, f), non_blocking=True)
             ids_static.copy_(ids_dev[t], non_blocking=True)
             graph.replay()
             nm_hist[t].copy_(nm_static, non_blocking=True)
+            miss_hist[t].copy_(st.miss, non_blocking=True)
 
-    # ---- warm-up, then the timed steps -----------------------------------------------------
-    # state snapshots at the start of the segments that are re-run with per-kernel events
+    # ---- warm-up, the timed steps, then the rest of the trace pass ------------------------
+    # state snapshots at the starts of the segments re-run with per-kernel events: the timed
+    # window's, and the steady-state window's (second half of the trace pass)
     nseg = max(1, min(args.timing_segments, K))
     seg_len = max(1, min(args.segment_steps, K // nseg))
-    seg_starts = [W + (k * (K - seg_len)) // max(1, nseg - 1) for k in range(nseg)] \
-        if nseg > 1 else [W]
-    snaps = {t: st.snapshot() for t in seg_starts}
-    run_steps(0, W)
+    seg_starts = _spread(W, T, nseg, seg_len)
+    late_len = min(args.segment_steps, max(1, (TP - late0) // max(1, args.timing_segments)))
+    late_starts = _spread(late0, TP, args.timing_segments, late_len) if TP - late0 >= 16 \
+        else []
+    pf0 = late0 if late_starts else W  # the prefetch leg starts from a steady state too
+    snaps = {t: st.snapshot() for t in set(seg_starts) | set(late_starts) | {W, pf0}}
+    run_steps(0, W, snaps)
     torch.cuda.synchronize()
     ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     wall0 = time.perf_counter()
     ev_a.record()
     run_steps(W, T, snaps)
     ev_b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    gpu_ms = ev_a.elapsed_time(ev_b)
-    elapsed_s = max(wall, gpu_ms / 1e3)
+    elapsed_s = max(wall, ev_a.elapsed_time(ev_b) / 1e3)
+    rest_s = 0.0
+    if TP > T:
+        wall0 = time.perf_counter()
+        ev_a.record()
+        run_steps(T, TP, snaps)
+        ev_b.record()
+        torch.cuda.synchronize()
+        rest_s = max(time.perf_counter() - wall0, ev_a.elapsed_time(ev_b) / 1e3)
     nm = nm_hist.cpu().numpy()
     inserts = int(nm[W:T].sum())
     distinct = int(_distinct(np, ids_np[W:T]).sum())
     gathered = inserts * B_exp
     value = gathered / elapsed_s / 1e9
-    log(f"timed: {K} steps in {elapsed_s:.2f}s ({1e3 * elapsed_s / K:.3f} ms/step), "
-        f"{inserts} inserts, {gathered / 1e9:.1f} GB -> {value:.2f} GB/s")
+    log(f"timed: {K} steps (trace steps {W}..{T}) in {elapsed_s:.2f}s "
+        f"({1e3 * elapsed_s / K:.3f} ms/step), {inserts} inserts, {gathered / 1e9:.1f} GB -> "
+        f"{value:.2f} GB/s")
+    pass_inserts = int(nm[W:TP].sum())
+    pass_s = elapsed_s + rest_s
+    trace_pass = {
+        "trace_steps": [W, TP], "ms_per_step": round(1e3 * pass_s / (TP - W), 4),
+        "GBps": round(pass_inserts * B_exp / pass_s / 1e9, 3), "inserts": pass_inserts,
+        "hit_rate": round(1.0 - pass_inserts / int(_distinct(np, ids_np[W:TP]).sum()), 5),
+        "hit_rate_from_cold_start": round(
+            1.0 - int(nm[:TP].sum()) / int(_distinct(np, ids_np[:TP]).sum()), 5),
+        "def": "the same graph replayed from step W to the end of the trace pass (the timed "
+               "steps included): whole-job GB/s and hit rate over those steps"}
+    log(f"trace pass: steps {W}..{TP} at {trace_pass['ms_per_step']} ms/step, "
+        f"{trace_pass['GBps']} GB/s, hit rate {trace_pass['hit_rate']}")
 
-    # ---- per-kernel durations: segments of the timed steps re-run from their snapshots, --
-    # ---- HIP events around every launch on the launch stream ----------------------------
+    # ---- verification of the trace pass's slot bytes (its state is checked against the ----
+    # ---- oracle in the cpu_baseline leg) -------------------------------------------------
     final = st.snapshot()
+    t1 = time.time()
+    slot_ok, resident = True, 0
+    for l in range(L):
+        for b, nb in enumerate(bufs):
+            ok, n = traces.slots_match(slots[l][b], st.slot_expert[l], content[l], b, nb)
+            slot_ok = slot_ok and ok
+        resident += n
+    log(f"verify: {resident} resident slots x {B_exp} B against the position hash: "
+        f"{'equal' if slot_ok else 'MISMATCH'} ({time.time() - t1:.1f}s)")
+    verified = {"slot_bytes": slot_ok, "resident_slots": resident,
+                "slot_bytes_checked": resident * B_exp, "layers": L, "trace_steps": [0, TP],
+                "state": None, "n_miss_per_step": None, "miss_lists_per_step": None,
+                "def": "after the trace pass: every resident slot's bytes against the "
+                       "position-hash content of the expert its slot_expert names; every "
+                       "layer's per-step n_miss and miss list and final state (table, "
+                       "map_cold, slot_expert, slot_stamp, step) against the oracle's policy "
+                       "step in C from the same cold start (cpu_baseline leg)"}
+
+    # ---- per-kernel durations: segments re-run from their snapshots, HIP events around ----
+    # ---- every launch on the launch stream ----------------------------------------------
     stream = torch.cuda.current_stream()
     s_ptr = ctypes.c_void_p(stream.cuda_stream)
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(seg_len)]
-    seg_out = torch.zeros((seg_len, L, mk), dtype=torch.int32, device=dev)
-    seg_nm = torch.zeros((seg_len, L), dtype=torch.int32, device=dev)
-    man_us, gat_us, wnm = [], [], []
-    for t0s in seg_starts:
-        st.restore(snaps[t0s])
-        torch.cuda.synchronize()
-        torch.cuda._sleep(int(2e8))  # hold the stream while the segment is queued behind it
-        for i in range(seg_len):
-            t = t0s + i
-            for l in range(L):
-                e0, e1, e2 = ev[i][l]
-                e0.record(stream)
-                rc = lib.expert_cache_manage_remap(
-                    *manage_args(l, row(ids_dev[t], l), row(seg_nm[i], l), row(seg_out[i], l)),
-                    s_ptr)
-                e1.record(stream)
-                rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
-                                              row(seg_nm[i], l), chunks, lanes, s_ptr)
-                e2.record(stream)
-                if rc:
-                    raise RuntimeError(f"launch failed rc={rc}")
-        torch.cuda.synchronize()
-        man_us.append([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
-                       for i in range(seg_len)])
-        gat_us.append([[ev[i][l][1].elapsed_time(ev[i][l][2]) * 1e3 for l in range(L)]
-                       for i in range(seg_len)])
-        got = seg_nm.cpu().numpy()
-        assert np.array_equal(got, nm[t0s:t0s + seg_len]), "segment diverged from timed run"
-        wnm.append(got)
+
+    def event_segments(starts, n):
+        ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+                torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(n)]
+        seg_out = torch.zeros((n, L, mk), dtype=torch.int32, device=dev)
+        seg_nm = torch.zeros((n, L), dtype=torch.int32, device=dev)
+        man, gat, wn = [], [], []
+        for t0s in starts:
+            st.restore(snaps[t0s])
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(2e8))  # hold the stream while the segment is queued
+            for i in range(n):
+                t = t0s + i
+                for l in range(L):
+                    e0, e1, e2 = ev[i][l]
+                    e0.record(stream)
+                    rc = lib.expert_cache_manage_remap(
+                        *manage_args(l, row(ids_dev[t], l), row(seg_nm[i], l),
+                                     row(seg_out[i], l)), s_ptr)
+                    e1.record(stream)
+                    rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
+                                                  row(seg_nm[i], l), chunks, lanes, s_ptr)
+                    e2.record(stream)
+                    if rc:
+                        raise RuntimeError(f"launch failed rc={rc}")
+            torch.cuda.synchronize()
+            man.append([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
+                        for i in range(n)])
+            gat.append([[ev[i][l][1].elapsed_time(ev[i][l][2]) * 1e3 for l in range(L)]
+                        for i in range(n)])
+            got = seg_nm.cpu().numpy()
+            assert np.array_equal(got, nm[t0s:t0s + n]), "segment diverged from the trace pass"
+            wn.append(got)
+        man, gat, wn = np.array(man), np.array(gat), np.array(wn)
+        with_miss = wn > 0
+        fig = {"achieved": wn.sum() * B_exp / (gat.sum() * 1e-6) / 1e9,
+               "with_miss": (wn[with_miss].sum() * B_exp / (gat[with_miss].sum() * 1e-6) / 1e9
+                             if with_miss.any() else None),
+               "zero_us": float(gat[~with_miss].mean()) if (~with_miss).any() else None,
+               "gather_us": float(gat.mean()), "manage_us": float(man.mean()),
+               "manage_p50": float(np.median(man)), "launches": int(wn.size),
+               "launches_with_miss": int(with_miss.sum()), "inserts": int(wn.sum())}
+        log(f"{len(starts)} segments x {n} steps from {starts[0]}: manage+remap "
+            f"{fig['manage_us']:.2f} us/layer (p50 {fig['manage_p50']:.2f}), gather "
+            f"{fig['gather_us']:.1f} us/launch, {fig['achieved']:.2f} GB/s over all launches, "
+            f"{fig['with_miss']} GB/s over launches with a miss, {fig['zero_us']} us for a "
+            f"launch with no miss")
+        return fig
+
+    tw = event_segments(seg_starts, seg_len)
+    late = event_segments(late_starts, late_len) if late_starts else None
     st.restore(final)
-    man_us, gat_us, wnm = np.array(man_us), np.array(gat_us), np.array(wnm)
-    miss_launch = wnm > 0
-    win_bytes = wnm.sum() * B_exp
-    achieved = win_bytes / (gat_us.sum() * 1e-6) / 1e9
-    per_miss = (wnm[miss_launch].sum() * B_exp / (gat_us[miss_launch].sum() * 1e-6) / 1e9
-                if miss_launch.any() else None)
-    zero_us = float(gat_us[~miss_launch].mean()) if (~miss_launch).any() else None
-    log(f"{nseg} segments x {seg_len} steps: manage+remap {man_us.mean():.2f} us/layer "
-        f"(p50 {np.median(man_us):.2f}), gather {gat_us.mean():.1f} us/launch, "
-        f"{achieved:.2f} GB/s over all launches, {per_miss} GB/s over launches with a miss, "
-        f"{gat_us[~miss_launch].mean() if (~miss_launch).any() else float('nan'):.2f} us "
-        f"for a launch with no miss")
 
     # ---- host->device link peak -------------------------------------------------------------
     n_peak = 256 << 20
@@ -432,6 +518,7 @@ def main():
     peak = max(memcpy_gbps, kernel_gbps)
     log(f"link peak: hipMemcpyAsync H2D {memcpy_gbps:.2f} GB/s, gather kernel on one 256 MB "
         f"slab {kernel_gbps:.2f} GB/s")
+    del src, dst
 
     # ---- latency floor: an empty kernel node in a graph (48 per replay) --------------------
     ge = torch.cuda.CUDAGraph()
@@ -449,35 +536,46 @@ def main():
     del ge
     log(f"empty kernel node in a graph: {empty_us:.2f} us")
 
-    # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer) --------------
+    # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer); the same --
+    # ---- C policy over the trace pass checks the GPU's states ----------------------------
     cpu = None
     if args.cpu_steps > 0:
-        cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
-                           policy, decay, W)
+        cpu, check = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E,
+                                  S, mk, policy, decay, W, TP, nm[:TP],
+                                  miss_hist.cpu().numpy(), final)
+        verified.update(check)
+    verified["all"] = all(verified[k] is not False for k in
+                          ("slot_bytes", "state", "n_miss_per_step", "miss_lists_per_step"))
 
     prefetch = None
     if not args.no_prefetch:
         # about 130 GB moved per run at most: 1,024 steps of the default workload, fewer
         # where experts are hundreds of MB
-        per_step = max(1.0, inserts * B_exp / K)
-        prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[W], L, E, S,
-                                mk, policy, decay, W, T, B_exp, chunks, lanes, dev, peak,
-                                window=max(32, min(1024, int(130e9 / per_step))))
+        per_step = max(1.0, pass_inserts * B_exp / (TP - W))
+        pw = max(32, min(1024, int(130e9 / per_step)))
+        prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[pf0], L, E, S,
+                                mk, policy, decay, pf0, min(steps, pf0 + pw), B_exp, chunks,
+                                lanes, dev, peak)
 
     fused = None if args.no_fused else fused_leg(torch, np, lib, dev)
 
     sweep = None
     if not args.no_hit_sweep:
         sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
-    manage_us = round(float(man_us.mean()), 3)
+    manage_us = round(tw["manage_us"], 3)
     manage_def = "HIP events around each launch (adds ~2 us per launch): an upper bound"
     for x in sweep or []:
         if x.get("slots") == S and x.get("policy") == args.policy:
             manage_us = x["graph_us_per_layer"]
-            manage_def = ("in-graph cost per layer of the policy+remap kernel alone over the "
-                          "whole trace at this budget and policy (hit-rate pass)")
+            manage_def = (f"in-graph cost per layer of the policy+remap kernel alone over the "
+                          f"whole {x['steps']}-step trace at this budget and policy "
+                          f"(hit-rate pass)")
 
     traffic = _traffic()
+
+    def rounded(v, n=3):
+        return None if v is None else round(v, n)
+
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -497,53 +595,116 @@ def main():
                    "slots": S, "policy": args.policy,
                    "decay": decay, "bytes_per_expert": B_exp, "host_store_GB":
                    round(L * E * B_exp / 1e9, 2), "host_store": host_store,
+                   "expert_content": "position hash of (layer, expert, buffer, word)",
                    "gather_grid": [chunks, lanes],
-                   "timed_trace_steps": [W, T]},
+                   "timed_trace_steps": [W, T], "trace_steps": steps},
+        "verified": verified,
         "hit_rate": round(1.0 - inserts / distinct, 5),
         "inserts": inserts,
+        "trace_pass": trace_pass,
         "manage_remap_us_per_layer": manage_us,
         "manage_remap_def": manage_def,
-        "manage_remap_us_per_layer_events": round(float(man_us.mean()), 3),
+        "manage_remap_us_per_layer_events": round(tw["manage_us"], 3),
         "empty_kernel_graph_us": round(empty_us, 3),
         "manage_remap_counters": _manage_counters(),
-        "gather_us_per_launch": round(float(gat_us.mean()), 3),
-        "gather_GBps_launches_with_miss": None if per_miss is None else round(per_miss, 3),
-        "gather_us_launch_without_miss": None if zero_us is None else round(zero_us, 3),
+        "gather_us_per_launch": round(tw["gather_us"], 3),
+        "gather_GBps_launches_with_miss": rounded(tw["with_miss"]),
+        "gather_us_launch_without_miss": rounded(tw["zero_us"]),
         "link_peak_GBps": {"hipMemcpyAsync_h2d": round(memcpy_gbps, 3),
                            "gather_kernel_256MB": round(kernel_gbps, 3)},
-        "roofline": {"bound": "host-link", "kernel": "gather_k", "achieved": round(achieved, 3),
-                     "peak": round(peak, 3), "unit": "GB/s", "frac": round(achieved / peak, 4),
-                     "achieved_launches_with_miss": None if per_miss is None
-                     else round(per_miss, 3),
-                     "frac_launches_with_miss": None if per_miss is None
-                     else round(per_miss / peak, 4),
+        "roofline": {"bound": "host-link", "kernel": "gather_k",
+                     "achieved": round(tw["achieved"], 3),
+                     "peak": round(peak, 3), "unit": "GB/s",
+                     "frac": round(tw["achieved"] / peak, 4),
+                     "achieved_launches_with_miss": rounded(tw["with_miss"]),
+                     "frac_launches_with_miss": None if tw["with_miss"] is None
+                     else round(tw["with_miss"] / peak, 4),
                      "traffic": None if traffic is None else traffic["bytes_per_launch"],
                      "traffic_detail": traffic,
                      "achieved_def": f"gathered bytes / summed gather kernel time over all "
-                                     f"launches, launches without a miss included, {nseg} "
-                                     f"segments x {seg_len} of the timed steps x {L} layers, "
+                                     f"launches, launches without a miss included, in the "
+                                     f"timed window (trace steps {W}..{T}"
+                                     f"{', a cold start' if W < 64 else ''}): {nseg} segments "
+                                     f"x {seg_len} steps x {L} layers re-run from snapshots, "
                                      f"HIP events around each launch; "
                                      f"achieved_launches_with_miss counts only launches that "
-                                     f"copy, gather_us_launch_without_miss is the rest's cost",
+                                     f"copy, gather_us_launch_without_miss is the rest's cost; "
+                                     f"steady_state is the same over the second half of the "
+                                     f"trace pass",
                      "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
-                                 "kernel on one 256 MB slab)"},
+                                 "kernel on one 256 MB slab)",
+                     "steady_state": None if late is None else {
+                         "trace_steps": [late0, TP], "segments": len(late_starts),
+                         "segment_steps": late_len, "achieved": round(late["achieved"], 3),
+                         "frac": round(late["achieved"] / peak, 4),
+                         "achieved_launches_with_miss": rounded(late["with_miss"]),
+                         "frac_launches_with_miss": None if late["with_miss"] is None
+                         else round(late["with_miss"] / peak, 4),
+                         "gather_us_launch_without_miss": rounded(late["zero_us"]),
+                         "inserts_per_launch": round(late["inserts"] / late["launches"], 4),
+                         "manage_remap_us_per_layer_events": round(late["manage_us"], 3)}},
         "cpu_baseline": cpu,
         "prefetch": prefetch,
         "fused": fused,
         "hit_rate_sweep": sweep,
     }
     print(json.dumps(res), flush=True)
+    if not verified["all"]:
+        log(f"VERIFICATION FAILED: {verified}")
+        sys.exit(1)
+
+
+def _spread(lo, hi, n, length):
+    """n segment starts of `length` steps spread evenly over [lo, hi)."""
+    n = max(1, n)
+    if n == 1 or hi - lo <= length:
+        return [lo]
+    return sorted({lo + (k * (hi - lo - length)) // (n - 1) for k in range(n)})
 
 
 def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, policy, decay,
-                 W):
-    """The CPU path on this host: the oracle's C policy (one core) decides each layer's
-    misses from the same start state, and each (miss, buffer) is one hipMemcpyAsync from
-    pinned host memory into the slot. Bounded sample: the first cpu_steps timed steps."""
+                 W, TP, gpu_nm, gpu_miss, gpu_final):
+    """The CPU path on this host, and the check of the GPU's trace pass.
+
+    Timed: the oracle's C policy (oracle/policy.c, one core) over the trace pass from a
+    cold start, every layer; the same over 16 host threads; and the CPU-driven cache over a
+    bounded sample (the first cpu_steps timed steps from the same start state): the C policy
+    decides each layer's misses and each (miss, buffer) is one hipMemcpyAsync from pinned
+    host memory into the slot.
+
+    Checked: the oracle's per-step n_miss and miss lists over the trace pass, and its final
+    state, against what the GPU's graph produced (gpu_nm [TP, L], gpu_miss [TP, L, 2S],
+    gpu_final the GPU state after step TP)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    n = min(args.cpu_steps, ids_np.shape[0] - W)
+    rows = [np.ascontiguousarray(ids_np[:TP, l]) for l in range(L)]
+    t0 = oracle.now()
+    runs = [oracle.run_trace(rows[l], E, S, policy, decay) for l in range(L)]
+    policy_us = (oracle.now() - t0) / (TP * L) * 1e6
+    # the same policy work spread over host threads, one layer at a time per thread (the C
+    # call releases the interpreter lock); layers are independent
+    from concurrent.futures import ThreadPoolExecutor
+    threads = max(1, min(16, os.cpu_count() or 1, L))
+    t0 = oracle.now()
+    with ThreadPoolExecutor(threads) as ex:
+        par = list(ex.map(lambda l: oracle.run_trace(rows[l], E, S, policy, decay,
+                                                     record_miss=True), range(L)))
+    policy_par_us = (oracle.now() - t0) / (TP * L) * 1e6
+
+    # the check: per-step n_miss and miss lists, then every final state field
+    nm_ok = all(np.array_equal(par[l]["n_miss"], gpu_nm[:, l]) for l in range(L))
+    miss_ok = all(np.array_equal(par[l]["miss"], gpu_miss[:, l]) for l in range(L))
+    fields = ("table", "map_cold", "slot_expert", "slot_stamp", "step")
+    got = {f: gpu_final[f].cpu().numpy() for f in fields}
+    state_ok = all(np.array_equal(getattr(runs[l]["final"], f).ravel(), got[f][l].ravel())
+                   and np.array_equal(getattr(par[l]["final"], f).ravel(), got[f][l].ravel())
+                   for l in range(L) for f in fields)
+    log(f"verify: oracle over {TP} steps x {L} layers: per-step n_miss "
+        f"{'equal' if nm_ok else 'MISMATCH'}, miss lists {'equal' if miss_ok else 'MISMATCH'}, "
+        f"final state {'equal' if state_ok else 'MISMATCH'}")
+    check = {"state": state_ok, "n_miss_per_step": nm_ok, "miss_lists_per_step": miss_ok}
+
     states = []
     for l in range(L):
         s = oracle.State(E, S)
@@ -554,25 +715,7 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         s.step[:] = snap["step"][l].cpu().numpy()
         states.append(s)
     B_exp = sum(bufs)
-    # policy alone, in C, over the sample (copies of the states, so the run below is fresh)
-    pol_states = [s.copy() for s in states]
-    t0 = oracle.now()
-    for l in range(L):
-        oracle.run_trace(np.ascontiguousarray(ids_np[W:W + n, l]), E, S, policy, decay,
-                         state=pol_states[l])
-    policy_us = (oracle.now() - t0) / (n * L) * 1e6
-    # the same policy work spread over host threads, one layer at a time per thread (the C
-    # call releases the interpreter lock); layers are independent
-    from concurrent.futures import ThreadPoolExecutor
-    threads = max(1, min(16, os.cpu_count() or 1, L))
-    par_states = [s.copy() for s in states]
-    t0 = oracle.now()
-    with ThreadPoolExecutor(threads) as ex:
-        list(ex.map(lambda l: oracle.run_trace(np.ascontiguousarray(ids_np[W:W + n, l]), E, S,
-                                               policy, decay, state=par_states[l]), range(L)))
-    policy_par_us = (oracle.now() - t0) / (n * L) * 1e6
-    for a_, b_ in zip(pol_states, par_states):
-        assert np.array_equal(a_.table, b_.table), "threaded policy diverged"
+    n = min(args.cpu_steps, ids_np.shape[0] - W)
     torch.cuda.synchronize()
     moved = 0
     t0 = time.perf_counter()
@@ -600,16 +743,17 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         f"{policy_par_us:.3f} us/layer-step over {threads} threads; host memcpy "
         f"{host_memcpy:.1f} GB/s")
     return {"value": round(moved / wall / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"timed steps {W}..{W + n} of the trace x {L} layers from the same start "
+            "sample": f"trace steps {W}..{W + n} x {L} layers from the timed steps' start "
                       f"state: C policy (oracle/policy.c) per layer-step, then one "
                       f"hipMemcpyAsync H2D per (miss, buffer)",
             "policy_us_per_layer_step": round(policy_us, 4),
+            "policy_sample": f"trace steps 0..{TP} x {L} layers from a cold start",
             "policy_us_per_layer_step_threads": round(policy_par_us, 4),
             "policy_threads": threads,
             "host_memcpy_GBps": round(host_memcpy, 2),
             "fused_us_per_layer_step": None if args.no_fused else _cpu_fused(np, oracle),
             "pcie_round_trip_us_per_layer_step": _pcie_round_trip(torch),
-            "cpu": _cpu_model(), "nproc": os.cpu_count()}
+            "cpu": _cpu_model(), "nproc": os.cpu_count()}, check
 
 
 def _pcie_round_trip(torch, n=2000):
@@ -756,8 +900,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                  configs=((None, 0, False, None), (1.0, 1, False, None), (1.0, 1, True, None),
                           (0.8, 1, True, None), (0.8, 1, True, 1), (1.0, 2, True, None),
                           (1.0, 4, True, None))):
-    """Prefetch over a window of the timed steps, every run from the same start state, as
-    one captured graph per decode step. With a lookahead of d layers:
+    """Prefetch over trace steps W..T, every run from the same start state (the snapshot
+    `snap` taken at step W of the trace pass), as one captured graph per decode step. With a lookahead of d layers:
       d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
       d >= 1: layers 0..d-1 prefetched first, then per layer l the prefetch step of layer
               l+d and manage+remap(l) -- two launches (expert_cache_prefetch, then

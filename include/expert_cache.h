@@ -46,7 +46,8 @@ int expert_cache_manage(const int* topk_ids, int mk, int E, int S, int max_disti
 /*
  * Copy every missing expert's slabs from host-readable memory into its slot: for
  * j < *n_miss and each of the six buffers, dst_b[slot_j] <- src_b[expert_j], b_b bytes per
- * expert. A buffer repeated with the same (dst, src, bytes) is copied once.
+ * expert. A buffer repeated with the same (dst, src, bytes) is copied once. `miss` is read
+ * only for j < *n_miss, so a list with no capacity is accepted while *n_miss is 0.
  * The grid is chunks x lanes workgroups of 256 lanes; the work (miss, buffer, tile) is
  * spread over the whole grid whatever n_miss is.
  * Fails with -1 unless every b_b > 0 and b_b % 16 == 0, chunks > 0 and lanes > 0.

@@ -219,22 +219,46 @@ def test_real_trace_suite(tmp_path, policy, lib_name):
     assert int(want["n_miss"].sum()) > 0
 
 
-REF_CASES = [("48-layer-e128", 16, "lfu"), ("48-layer-e128", 64, "lfu"),
-             ("48-layer-e128", 64, "lru"), ("48-layer-e128-batch4", 32, "lfu"),
-             ("8-layer-e256-fp8", 128, "lru")]
+REF_CASES = [("48-layer-e128", 16, "lfu", 2048), ("48-layer-e128-batch4", 32, "lfu", 2048),
+             ("8-layer-e256-fp8", 128, "lru", 2048)]
 
 
-@pytest.mark.parametrize("name,slots,policy", REF_CASES)
-def test_reference_kernel_agrees_with_oracle(name, slots, policy):
+@pytest.mark.parametrize("name,slots,policy,steps", REF_CASES)
+def test_reference_kernel_agrees_with_oracle(name, slots, policy, steps):
     """The reference's own kernel on the workloads: pins the oracle to the reference."""
     h = gu.ref_lib()
     if h is None:
         pytest.skip("reference library not built")
     w = traces.WORKLOADS[name]
-    ids = traces.routing_all_layers(w, steps=min(w.steps, 2048))
+    ids = traces.routing_all_layers(w, steps=min(w.steps, steps))
     got = gu.run_trace(h, ids, w.experts, slots, POLICY[policy])
     want = gu.oracle_trace(ids, w.experts, slots, POLICY[policy])
     _assert_same(got, want, ("n_miss", "miss", "state"), f"reference:{name}")
+
+
+@pytest.mark.parametrize("policy", ["lfu", "lru"])
+def test_product_equals_reference_kernel_over_the_whole_trace(policy):
+    """The benchmark workload at its 64-slot budget, all 48 layers x 4096 steps from a cold
+    start: the reference's kernel, this library's product entry point (policy step + fused
+    remap) and the oracle, compared on every field of every step. The product is compared
+    with the reference's kernel directly, not only through the oracle, and its slot ids
+    with the reference's table after each step (cache.py:108-110 of the reference)."""
+    h = gu.ref_lib()
+    if h is None:
+        pytest.skip("reference library not built")
+    w = traces.WORKLOADS["48-layer-e128"]
+    ids = traces.routing_all_layers(w)
+    assert ids.shape == (4096, 48, 8)
+    ref = gu.run_trace(h, ids, w.experts, 64, POLICY[policy])
+    got = gu.run_trace(gu.lib(), ids, w.experts, 64, POLICY[policy], fused_remap=True)
+    _assert_same(got, ref, ("n_miss", "miss", "state"), f"product-vs-reference:{policy}")
+    _assert_same({"out": got["out"]}, {"out": _expected_remap(ids, ref["state"], w.experts)},
+                 ("out",), f"product-vs-reference:{policy}")
+    del got
+    want = gu.oracle_trace(ids, w.experts, 64, POLICY[policy])
+    _assert_same(ref, want, ("n_miss", "miss", "state"), f"reference-vs-oracle:{policy}")
+    print(f"whole trace {policy}: {int(want['n_miss'].sum())} inserts over "
+          f"{ids.shape[0]} x {ids.shape[1]} layer-steps, identical", flush=True)
 
 
 def test_deterministic_across_runs():

@@ -15,10 +15,11 @@ captured in HIP graphs so that host launch cost is out of the picture:
     its batch-4 form (48 slots), 352 MB bf16 experts (4 slots) and 44 MB fp8 experts
     (4 layers, 128 slots, 128 ids per step).
 
-Each test prints one "speed:" line per figure (run pytest with -s to see them) and asserts
-this library is not slower than the reference beyond a 10 % noise margin. EC_SPEED_ASSERT=0
-keeps only the byte checks (for runs under a profiler, whose per-dispatch cost swamps
-kernels of a few microseconds).
+Each test prints one "speed:" line per figure (run pytest with -s to see them). The byte
+checks are the gate. The times are reported, not asserted: EC_SPEED_ASSERT=1 turns on a
+regression guard (this library not slower than the reference beyond a 10 % noise margin),
+for a quiet machine and not under a profiler, whose per-dispatch cost swamps kernels of a
+few microseconds.
 """
 from __future__ import annotations
 
@@ -40,7 +41,7 @@ REF_CHUNKS, REF_LANES = 16, 64      # vllm_expert_cache/cache.py:96-97 of the re
 REF_SIZES = (819200, 409600, 51200, 640, 25600, 2560)   # tests/test_policy.py:237
 
 
-SPEED_ASSERT = os.environ.get("EC_SPEED_ASSERT", "1") != "0"
+SPEED_ASSERT = os.environ.get("EC_SPEED_ASSERT", "0") == "1"
 # a regression guard, not the measurement (the timings are printed): the closest case, the
 # 44 MB experts where both sides run at the link's rate, is a tie, so leave room for noise
 MARGIN = 1.10

@@ -94,3 +94,40 @@ def test_bench_counts_distinct_experts_without_padding():
     big = rng.integers(-1, 40, size=(50, 3, 12)).astype(np.int32)
     want = [[len(set(r[r >= 0].tolist())) for r in step] for step in big]
     assert bench._distinct(np, big).tolist() == want
+
+
+def test_position_hash_content_detects_misplaced_bytes():
+    """The synthetic expert content the bench verifies slots against: every word differs
+    within a slab and across experts, layers and buffers; chunked generation equals one-shot
+    generation; and a slot holding another expert's row, another layer's, or one 16-byte
+    vector shifted is reported as a mismatch."""
+    import torch
+
+    from vllm_expert_cache import traces
+
+    nbytes, E = 256, 6
+    rows = {(l, b): traces.expert_words(l, range(E), b, nbytes, "cpu")
+            for l in (0, 1) for b in (0, 1)}
+    allw = torch.cat([r.flatten() for r in rows.values()])
+    assert allw.unique().numel() == allw.numel()
+    part = traces.expert_words(1, [4], 1, nbytes, "cpu", first_word=8, nwords=20)
+    assert torch.equal(part[0], rows[(1, 1)][4, 8:28])
+    store = torch.empty(E * nbytes, dtype=torch.uint8)
+    traces.fill_expert_store(store, 1, 0, nbytes, E, "cpu", chunk_words=7)
+    assert torch.equal(store.view(torch.int32).view(E, -1), rows[(1, 0)])
+
+    se = torch.tensor([2, -1, 5, 0], dtype=torch.int32)
+    slots = torch.zeros(4, nbytes // 4, dtype=torch.int32)
+    for s, e in enumerate(se.tolist()):
+        if e >= 0:
+            slots[s] = rows[(1, 0)][e]
+    flat = slots.view(torch.uint8).flatten()
+    for cw in (3, 64, 1 << 20):
+        assert traces.slots_match(flat, se, 1, 0, nbytes, chunk_words=cw) == (True, 3)
+    bad = [slots.clone() for _ in range(3)]
+    bad[0][2] = rows[(1, 0)][4]                     # another expert's row
+    bad[1][0] = rows[(0, 0)][2]                     # the same expert of another layer
+    bad[2][3, 8:12] = rows[(1, 0)][0, 12:16]        # one 16-byte vector shifted
+    for b in bad:
+        assert traces.slots_match(b.view(torch.uint8).flatten(), se, 1, 0, nbytes,
+                                  chunk_words=3)[0] is False

@@ -101,20 +101,16 @@ __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
                                                            const int* __restrict__ miss,
                                                            const int* __restrict__ n_miss) {
   const long long per = g.per;
-  const long long nblk = (long long)gridDim.x * gridDim.y;
   const long long t0 = (long long)blockIdx.y * gridDim.x + blockIdx.x;
-  // The first miss pair is read together with n_miss (the miss list always holds one
-  // pair): when this workgroup's first tile is in miss 0 -- every workgroup, once an expert
-  // spans more tiles than the grid has workgroups -- no second round trip is needed.
-  int nm = n_miss[0], e0 = miss[0], sl0 = miss[1];
-  // nothing may use the three values before this point: their loads go out together
-  asm volatile("" : "+s"(nm), "+s"(e0), "+s"(sl0));
+  // The miss list is read only below n_miss, as kernels/expert_cache.hip:294-298 reads it:
+  // a caller with no insert capacity (max_inserts = 0) may pass an empty list.
+  const int nm = n_miss[0];
   if (nm <= 0 || per <= 0 || t0 >= (long long)nm * per) return;
   const long long jstep = g.jstep, rstep = g.rstep;
   // first tile: in miss 0 whenever a miss spans more tiles than the grid has workgroups
   int j = t0 < per ? 0 : (int)(t0 / per);
   long long r = t0 - (long long)j * per;
-  int e = j == 0 ? e0 : miss[2 * j], sl = j == 0 ? sl0 : miss[2 * j + 1];
+  int e = miss[2 * j], sl = miss[2 * j + 1];
   GatherTile cur = gather_tile<U>(g, e, sl, r);
   u32x4 v[U];
   tile_load<U, NT_LOAD>(cur, v);

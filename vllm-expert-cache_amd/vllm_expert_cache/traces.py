@@ -144,3 +144,90 @@ def load_routes(path: str) -> np.ndarray:
 
 def save_routes(path: str, ids: np.ndarray) -> None:
     np.savez(path, ids=np.asarray(ids, dtype=np.int32))
+
+
+# ---- synthetic expert content ------------------------------------------------------------
+# Every 4-byte word of a synthetic expert slab is a hash of its position: (layer, expert,
+# buffer, word). A copy that lands in the wrong slot, takes another expert's or layer's row,
+# or shifts any 16-byte vector within a slab therefore shows up as a mismatch, which random
+# or constant bytes would not guarantee.
+
+_M32 = 0xFFFFFFFF
+_MUL = 0x045D9F3B  # odd: multiplication by it is a bijection mod 2**32
+
+
+def _mix32(x):
+    """A bijective 32-bit mixer (xor-shift, odd multiply, twice, then xor-shift) on int64
+    tensors holding values below 2**32: every product stays below 2**59."""
+    x = ((x ^ (x >> 16)) * _MUL) & _M32
+    x = ((x ^ (x >> 16)) * _MUL) & _M32
+    return x ^ (x >> 16)
+
+
+def expert_words(layer: int, experts, buffer: int, nbytes: int, device, first_word: int = 0,
+                 nwords: int | None = None):
+    """Synthetic content of `buffer`'s slab for each expert in `experts` of `layer`, as
+    int32 words [len(experts), nwords] (words first_word .. of a slab of nbytes, which must
+    be a multiple of 4). Requires layer < 2048, buffer < 16, expert ids in [0, 65536)."""
+    import torch
+
+    if nbytes % 4 or not (0 <= layer < 2048 and 0 <= buffer < 16):
+        raise ValueError("expert_words: nbytes % 4, layer or buffer out of range")
+    n = nbytes // 4 - first_word if nwords is None else int(nwords)
+    e = torch.as_tensor(experts, dtype=torch.int64, device=device).reshape(-1, 1)
+    if e.numel() and (int(e.min()) < 0 or int(e.max()) >= 65536):
+        raise ValueError("expert_words: expert id out of range")
+    seed = _mix32((layer << 20) ^ (buffer << 16) ^ e)
+    w = torch.arange(first_word, first_word + n, dtype=torch.int64, device=device).reshape(1, -1)
+    h = _mix32(w ^ seed)
+    h = _mix32((h + seed) & _M32)
+    return h.to(torch.int32)
+
+
+def fill_expert_store(host, layer: int, buffer: int, nbytes: int, experts: int, device,
+                      chunk_words: int = 1 << 26) -> None:
+    """Write expert_words of experts 0..experts-1 into `host` (a [experts * nbytes] uint8
+    tensor, pinned or on the device), generated on `device` in chunks of at most
+    chunk_words words."""
+    import torch
+
+    view = host.view(torch.int32).view(experts, nbytes // 4)
+    per = nbytes // 4
+    if per <= chunk_words:
+        step = max(1, chunk_words // per)
+        for e0 in range(0, experts, step):
+            e1 = min(experts, e0 + step)
+            view[e0:e1].copy_(expert_words(layer, range(e0, e1), buffer, nbytes, device))
+    else:
+        for e in range(experts):
+            for w0 in range(0, per, chunk_words):
+                n = min(chunk_words, per - w0)
+                view[e, w0:w0 + n].copy_(expert_words(layer, [e], buffer, nbytes, device,
+                                                      w0, n)[0])
+
+
+def slots_match(slot_buf, slot_expert, layer: int, buffer: int, nbytes: int,
+                chunk_words: int = 1 << 26) -> tuple[bool, int]:
+    """Does every resident slot of `slot_buf` ([S * nbytes] uint8 on the device) hold its
+    expert's expert_words? slot_expert: [S] int32 tensor (-1 for an empty slot). Returns
+    (all equal, slots compared)."""
+    import torch
+
+    per = nbytes // 4
+    view = slot_buf.view(torch.int32).view(-1, per)
+    se = slot_expert.to(torch.int64)
+    resident = torch.nonzero(se >= 0).flatten()
+    experts = se[resident]
+    ok = True
+    if per <= chunk_words:
+        step = max(1, chunk_words // per)
+        for i in range(0, resident.numel(), step):
+            want = expert_words(layer, experts[i:i + step], buffer, nbytes, slot_buf.device)
+            ok = ok and bool(torch.equal(view[resident[i:i + step]], want))
+    else:
+        for s, e in zip(resident.tolist(), experts.tolist()):
+            for w0 in range(0, per, chunk_words):
+                n = min(chunk_words, per - w0)
+                want = expert_words(layer, [e], buffer, nbytes, slot_buf.device, w0, n)[0]
+                ok = ok and bool(torch.equal(view[s, w0:w0 + n], want))
+    return ok, int(resident.numel())
