@@ -1,223 +1,311 @@
-"""Arming the slot cache on vLLM MoE layers, for any quantisation scheme.
+"""Arming the slot cache on vLLM MoE layers, whatever the quantisation scheme.
 
-Behaviour follows vllm_expert_cache/backends/generic.py:1-361 of the reference; this is
-the boundary the plugin keeps, not part of the accelerated path. It relies on three things
-every vLLM `FusedMoEMethodBase` subclass does:
+The observable behaviour is the reference's vllm_expert_cache/backends/generic.py:1-361:
+which layers are armed, which tensors are mirrored, the log lines, and the keyword
+signature of the wrapped `apply`. It is the plugin boundary the accelerated path keeps.
+
+How a layer is served from slots. vLLM's `FusedMoEMethodBase` subclasses share three
+habits, and the cache needs nothing else:
 
   * `apply` reads the expert weights off the layer (layer.w13_weight, layer.w2_weight);
-  * `get_fused_moe_quant_config(layer)` rebuilds the per-expert scales / zero points /
-    biases by reading named layer attributes;
-  * the built kernel keeps that config in `moe_kernel.fused_experts.quant_config`.
+  * `get_fused_moe_quant_config(layer)` rebuilds the per-expert scales, zero points and
+    biases by reading layer attributes;
+  * the built kernel holds that config in `moe_kernel.fused_experts.quant_config`.
 
-So a cached step points every per-expert attribute at its slot buffer, swaps in a config
-built against those buffers, narrows `global_num_experts` to the slot count and calls the
-stock `apply` with slot-space ids. Layers the cache cannot serve correctly are declined with
-a logged reason and keep running on the stock path.
+Arming is a plan that either completes or stops with a reason (`_Declined`):
+
+  1. find the expert weight pair, and the slot budget (nothing to do if every expert fits);
+  2. refuse layouts the cache cannot serve correctly (`_UNSUPPORTED`);
+  3. collect every expert-indexed storage of the layer (`_Mirror`: one storage, every name
+     that reaches it), build the cache over them, and decide what each name is rebound to;
+  4. ask the method for its config with the layer pointing at the slots, and refuse the
+     layer if that config still holds a full [E] tensor (slot ids would index it);
+  5. wrap the method's `apply` for this instance only.
+
+A served step applies one `_Patch` (slot tensors, slot config, slot count) around the stock
+`apply` and undoes it in reverse order, also when `apply` raises.
 """
 from __future__ import annotations
 
-import contextlib
-import itertools
+import functools
 import sys
+from dataclasses import dataclass, field
 
 import torch
 
 from ..cache import ExpertSlotCache
 from ..config import settings
 
-# FusedMoEQuantDesc fields that may hold a per-expert tensor, and the descs of a config
-_DESC_FIELDS = ("scale", "alpha_or_gscale", "zp", "bias")
-_DESC_NAMES = ("_a1", "_a2", "_w1", "_w2")
-
+# The two expert weight matrices, in the spellings vLLM schemes register: the plain one,
+# and the packed compressed-tensors one (wNa16 int4, w4a4 nvfp4 / mxfp4).
 _WEIGHT_PAIRS = (("w13_weight", "w2_weight"), ("w13_weight_packed", "w2_weight_packed"))
+
+# Where a FusedMoEQuantConfig keeps per-tensor descriptors, and the descriptor fields that
+# can hold a per-expert tensor (vLLM's interface).
+_CONFIG_DESCS = ("_a1", "_a2", "_w1", "_w2")
+_DESC_TENSORS = ("scale", "alpha_or_gscale", "zp", "bias")
 
 _installed = False
 
 
-def _set_tensor(layer, name: str, t: torch.Tensor) -> None:
-    """Rebind `layer.<name>` through the registry it lives in (a bare tensor cannot be
-    assigned over a registered Parameter)."""
-    if name in layer._parameters:
-        layer._parameters[name] = t
-    elif name in layer._buffers:
-        layer._buffers[name] = t
-    else:
-        setattr(layer, name, t)
+class _Declined(Exception):
+    """The layer stays on the stock path. `reason`, when given, is logged as a warning."""
+
+    def __init__(self, reason: str | None = None):
+        super().__init__(reason)
+        self.reason = reason
 
 
-def _per_expert_tensors(layer, num_experts: int) -> dict[str, list[str]]:
-    """Every expert-indexed storage of the layer (dim 0 == E), with all the names that reach
-    it: registered parameters and buffers, and plain tensor attributes. Aliases of one
-    storage (`layer.w13_weight = layer.w13_weight_packed`) form one group keyed by its first
-    name, so each storage is mirrored once and every alias is rebound."""
-    groups: dict[int, list[str]] = {}
-    named = itertools.chain(
-        # remove_duplicate=False: an aliased Parameter is registered under two names and
-        # must be found under both
-        layer.named_parameters(recurse=False, remove_duplicate=False),
-        layer.named_buffers(recurse=False, remove_duplicate=False),
-        ((k, v) for k, v in vars(layer).items() if isinstance(v, torch.Tensor)),
-    )
-    for name, t in named:
-        if not (isinstance(t, torch.Tensor) and t.dim() >= 1 and t.size(0) == num_experts):
-            continue
-        names = groups.setdefault(t.data_ptr(), [])
-        if name not in names:
-            names.append(name)
-    return {names[0]: names for names in groups.values()}
+# Layouts the cache cannot serve, checked in this order: (test, reason).
+_UNSUPPORTED = (
+    # apply_monolithic() routes internally: there are no topk_ids to move into slot space
+    (lambda layer, m: m.is_monolithic,
+     "monolithic method (routing happens inside apply_monolithic)"),
+    (lambda layer, m: getattr(m, "moe_kernel", None) is None,
+     "method has no moe_kernel (legacy non-modular path)"),
+    (lambda layer, m: getattr(m.moe_kernel, "fused_experts", None) is None,
+     "moe_kernel exposes no fused_experts to rebind"),
+    # with expert parallelism, expert_map folds global ids into a local range; composing it
+    # with the slot table would be a second remap
+    (lambda layer, m: getattr(layer, "expert_map", None) is not None,
+     "expert parallelism active (layer.expert_map is set)"),
+)
 
 
-def _leaked_full_tensors(cfg, num_experts: int) -> list[str]:
-    """Per-expert tensors a slot-bound config still takes from full [E] storage. Serving such
-    a layer would index expert rows with slot ids -- silently wrong -- so it is declined."""
-    leaked = []
-    for dname in _DESC_NAMES:
+@dataclass
+class _Mirror:
+    """One expert-indexed storage of the layer and every attribute name that reaches it, in
+    discovery order. The first name is where the cache reads the source from."""
+
+    names: list = field(default_factory=list)
+
+    @property
+    def source(self) -> str:
+        return self.names[0]
+
+
+def _is_expert_indexed(value, num_experts: int) -> bool:
+    return isinstance(value, torch.Tensor) and value.dim() >= 1 and \
+        value.size(0) == num_experts
+
+
+def _mirrors(layer, num_experts: int) -> list[_Mirror]:
+    """Every storage of the layer whose dim 0 is the expert count, with all its names.
+
+    Three registries are read, in this order: registered parameters, registered buffers,
+    and plain tensor attributes. The last matters for packed schemes that alias a
+    registered tensor under the name `apply` reads (layer.w13_weight =
+    layer.w13_weight_packed): both names must be rebound, or apply would keep reading full
+    storage with slot ids. Aliases share a storage, so they share one mirror and one slot
+    buffer. A dim-0 match that is not really per expert only costs memory; one missed is
+    caught by the config check."""
+    by_storage: dict[int, _Mirror] = {}
+    for registry in (layer._parameters, layer._buffers, vars(layer)):
+        for name, value in registry.items():
+            if _is_expert_indexed(value, num_experts):
+                mirror = by_storage.setdefault(value.data_ptr(), _Mirror())
+                if name not in mirror.names:
+                    mirror.names.append(name)
+    return list(by_storage.values())
+
+
+def _weight_pair(layer) -> tuple[str, str]:
+    for pair in _WEIGHT_PAIRS:
+        if all(isinstance(getattr(layer, n, None), torch.Tensor) for n in pair):
+            return pair
+    registered = sorted(n for n, _ in layer.named_parameters(recurse=False))
+    if any("w13" in n or "w2" in n for n in registered):
+        # name what is there: a naming convention, not a broken checkpoint
+        raise _Declined("no recognised expert weight pair; the layer registers "
+                        + (", ".join(registered) or "nothing"))
+    raise _Declined()  # not an expert layer this backend knows: nothing to say
+
+
+def _full_storage_in(cfg, num_experts: int):
+    """Descriptor fields of a quant config that still hold a full [E] tensor."""
+    for dname in _CONFIG_DESCS:
         desc = getattr(cfg, dname, None)
-        if desc is None:
+        for fname in _DESC_TENSORS if desc is not None else ():
+            t = getattr(desc, fname, None)
+            if _is_expert_indexed(t, num_experts):
+                yield f"{dname}.{fname}{tuple(t.shape)}"
+
+
+def _rebind(layer, name: str, value) -> None:
+    """layer.<name> = value, through the registry that holds the name (a bare tensor cannot
+    be assigned over a registered Parameter with setattr)."""
+    for registry in (layer._parameters, layer._buffers):
+        if name in registry:
+            registry[name] = value
+            return
+    setattr(layer, name, value)
+
+
+class _Patch:
+    """Attribute replacements applied one by one and undone in reverse order."""
+
+    __slots__ = ("_undo",)
+
+    def __init__(self):
+        self._undo = []
+
+    def set(self, obj, name: str, value) -> None:
+        self._undo.append((setattr, obj, name, getattr(obj, name)))
+        setattr(obj, name, value)
+
+    def tensor(self, layer, name: str, value) -> None:
+        self._undo.append((_rebind, layer, name, getattr(layer, name)))
+        _rebind(layer, name, value)
+
+    def slots(self, layer, bound: dict) -> None:
+        for name, t in bound.items():
+            self.tensor(layer, name, t)
+
+    def undo(self) -> None:
+        while self._undo:
+            restore, obj, name, old = self._undo.pop()
+            restore(obj, name, old)
+
+
+def _bindings(layer, mirrors: list[_Mirror], slots: dict) -> dict:
+    """What each mirrored name points at during a served step: its storage's slot buffer,
+    wrapped once as a Parameter for names registered as parameters (graph capture sees
+    fixed objects), bare for buffers and plain attributes."""
+    bound = {}
+    for m in mirrors:
+        slot = slots.get(m.source)
+        if slot is None:  # not 16-byte aligned per expert: left on full storage
             continue
-        for field in _DESC_FIELDS:
-            t = getattr(desc, field, None)
-            if isinstance(t, torch.Tensor) and t.dim() >= 1 and t.size(0) == num_experts:
-                leaked.append(f"{dname}.{field}{tuple(t.shape)}")
-    return leaked
+        as_param = torch.nn.Parameter(slot, requires_grad=False)
+        for name in m.names:
+            bound[name] = as_param if name in layer._parameters else slot
+    return bound
 
 
-@contextlib.contextmanager
-def _slot_bound(layer, cache: ExpertSlotCache):
-    """Point every mirrored attribute at its slot buffer inside the block, then restore."""
-    saved = {name: getattr(layer, name) for name in cache.bound}
-    try:
-        for name, slot in cache.bound.items():
-            _set_tensor(layer, name, slot)
-        yield
-    finally:
-        for name, t in saved.items():
-            _set_tensor(layer, name, t)
-
-
-def _decline(layer, method, num_experts: int) -> str | None:
-    """Why this layer cannot be cached correctly, or None."""
-    if method.is_monolithic:
-        return "monolithic method (routing happens inside apply_monolithic)"
-    if getattr(method, "moe_kernel", None) is None:
-        return "method has no moe_kernel (legacy non-modular path)"
-    if getattr(method.moe_kernel, "fused_experts", None) is None:
-        return "moe_kernel exposes no fused_experts to rebind"
-    if getattr(layer, "expert_map", None) is not None:
-        # EP folds global ids into a local range with expert_map; composing that with the
-        # slot table is a second remap this cache does not do
-        return "expert parallelism active (layer.expert_map is set)"
-    return None
-
-
-def _weight_names(layer) -> tuple[str, str] | None:
-    """Registered names of the two expert weight matrices (plain or packed spelling)."""
-    for a, b in _WEIGHT_PAIRS:
-        if isinstance(getattr(layer, a, None), torch.Tensor) and \
-                isinstance(getattr(layer, b, None), torch.Tensor):
-            return a, b
-    return None
-
-
-def arm(layer, method, logger) -> bool:
-    """Attach a slot cache to one MoE layer. Returns True if the cache is live."""
-    names = _weight_names(layer)
-    if names is None:
-        present = sorted(n for n, _ in layer.named_parameters(recurse=False))
-        if any("w13" in n or "w2" in n for n in present):
-            logger.warning(
-                "expert-cache: not caching %s -- no recognised expert weight pair; the layer "
-                "registers %s", type(method).__name__, ", ".join(present) or "nothing")
-        return False
-    w13_name, w2_name = names
-
-    num_experts = getattr(layer, w13_name).size(0)
+def _plan(layer, method, logger):
+    """Steps 1-4 of arming. Returns (cache, config built against the slots)."""
+    w13, w2 = _weight_pair(layer)
+    num_experts = getattr(layer, w13).size(0)
     slots = settings.slots_for(num_experts)
     if slots >= num_experts:
-        return False  # everything fits already; slots would only duplicate memory
+        raise _Declined()  # every expert fits: slots would only duplicate memory
+    for unsupported, reason in _UNSUPPORTED:
+        if unsupported(layer, method):
+            raise _Declined(reason)
 
-    reason = _decline(layer, method, num_experts)
-    if reason is not None:
-        logger.warning("expert-cache: not caching %s -- %s", type(method).__name__, reason)
-        return False
-
-    sources = _per_expert_tensors(layer, num_experts)
-    reachable = {n: key for key, group in sources.items() for n in group}
-    for name in (w13_name, w2_name):
-        if name not in reachable:
-            logger.warning(
-                "expert-cache: not caching %s -- %s is not a directly-owned expert-major "
-                "tensor (found: %s)", type(method).__name__, name,
-                ", ".join(sorted(reachable)) or "none")
-            return False
-    w13_key, w2_key = reachable[w13_name], reachable[w2_name]
-
+    mirrors = _mirrors(layer, num_experts)
+    owner = {name: m for m in mirrors for name in m.names}
+    for name in (w13, w2):
+        if name not in owner:
+            raise _Declined(f"{name} is not a directly-owned expert-major tensor (found: "
+                            f"{', '.join(sorted(owner)) or 'none'})")
     try:
-        cache = ExpertSlotCache(layer, sources.keys(), num_experts, slots,
-                                getattr(layer, w13_name).device,
-                                required=set(sources[w13_key]) | set(sources[w2_key]))
-    except ValueError as e:
-        logger.warning("expert-cache: not caching %s -- %s", type(method).__name__, e)
-        return False
-
-    # One slot buffer per storage, shared by all its aliases; wrapped as a Parameter once,
-    # and only for names registered as parameters.
-    cache.bound = {}
-    for canonical, group in sources.items():
-        if canonical not in cache.slots:
-            continue  # not 16-byte aligned: left on full storage for the leak check
-        slot = cache.slots[canonical]
-        as_param = torch.nn.Parameter(slot, requires_grad=False)
-        for name in group:
-            cache.bound[name] = as_param if name in layer._parameters else slot
-
+        # slots live on the weights' device at load time (the offloader moves the sources
+        # to host memory only afterwards)
+        cache = ExpertSlotCache(layer, [m.source for m in mirrors], num_experts, slots,
+                                getattr(layer, w13).device,
+                                required=set(owner[w13].names) | set(owner[w2].names))
+    except ValueError as e:  # a weight slab the 16-byte gather cannot move
+        raise _Declined(str(e)) from None
+    cache.bound = _bindings(layer, mirrors, cache.slots)
     if cache.skipped:
         logger.info("expert-cache: not mirroring %s (not 16-byte aligned per expert); the "
                     "leak check below decides whether that matters", ", ".join(cache.skipped))
 
-    with _slot_bound(layer, cache):
+    probe = _Patch()
+    try:
+        probe.slots(layer, cache.bound)
         slot_cfg = method.get_fused_moe_quant_config(layer)
+    finally:
+        probe.undo()
+    leaked = [] if slot_cfg is None else list(_full_storage_in(slot_cfg, num_experts))
+    if leaked:
+        raise _Declined(f"these per-expert tensors stayed bound to full [{num_experts}] "
+                        f"storage after slot binding and would be indexed by slot id: "
+                        f"{', '.join(leaked)}")
+    return cache, slot_cfg
 
-    if slot_cfg is not None:
-        leaked = _leaked_full_tensors(slot_cfg, num_experts)
-        if leaked:
-            logger.warning(
-                "expert-cache: not caching %s -- these per-expert tensors stayed bound to full "
-                "[%d] storage after slot binding and would be indexed by slot id: %s",
-                type(method).__name__, num_experts, ", ".join(leaked))
-            return False
 
-    orig_apply = method.apply
+def _serve_from_slots(layer, method, cache: ExpertSlotCache, slot_cfg) -> None:
+    """Step 5: wrap this method instance's apply."""
+    stock_apply = method.apply
 
-    # vLLM calls apply by keyword, so these parameter names are part of the contract.
+    # vLLM calls apply by keyword: these parameter names are the contract
     def apply(layer, x, topk_weights, topk_ids, shared_experts=None,
               shared_experts_input=None):
         if not cache.fits(topk_ids):
-            # wide (prefill) step: read through the host copies on the stock path; a
-            # prefetch still copying is joined so no side-stream work is left behind
+            # a wide (prefill) step reads through the full tensors on the stock path; a
+            # prefetch copy still in flight is joined so no side-stream work outlives it
             cache.join()
-            return orig_apply(layer, x, topk_weights, topk_ids, shared_experts,
-                              shared_experts_input)
+            return stock_apply(layer, x, topk_weights, topk_ids, shared_experts,
+                               shared_experts_input)
         slot_ids = cache.refresh(topk_ids)
-        experts = method.moe_kernel.fused_experts
-        saved = (experts.quant_config, method.moe_quant_config, layer.global_num_experts)
-        experts.quant_config = slot_cfg
-        method.moe_quant_config = slot_cfg
-        layer.global_num_experts = cache.S
+        patch = _Patch()
         try:
-            with _slot_bound(layer, cache):
-                return orig_apply(layer, x, topk_weights, slot_ids, shared_experts,
-                                  shared_experts_input)
+            patch.set(method.moe_kernel.fused_experts, "quant_config", slot_cfg)
+            patch.set(method, "moe_quant_config", slot_cfg)
+            patch.set(layer, "global_num_experts", cache.S)
+            patch.slots(layer, cache.bound)
+            return stock_apply(layer, x, topk_weights, slot_ids, shared_experts,
+                               shared_experts_input)
         finally:
-            experts.quant_config, method.moe_quant_config, layer.global_num_experts = saved
+            patch.undo()
 
     method.apply = apply
     layer._expert_cache = cache
+
+
+def arm(layer, method, logger) -> bool:
+    """Attach a slot cache to one MoE layer. Returns True if the cache is live."""
+    try:
+        cache, slot_cfg = _plan(layer, method, logger)
+    except _Declined as d:
+        if d.reason:
+            logger.warning("expert-cache: not caching %s -- %s", type(method).__name__,
+                           d.reason)
+        return False
+    _serve_from_slots(layer, method, cache, slot_cfg)
     return True
 
 
+def _arm_model(model, method_base, logger) -> None:
+    """Arm every MoE layer of a loaded model and log one summary line."""
+    armed: list = []
+    declined = 0
+    served_by: set[int] = set()  # method instances already wrapped
+    for _, module in model.named_modules():
+        method = getattr(module, "quant_method", None)
+        if not isinstance(method, method_base):
+            continue
+        if id(method) in served_by:
+            # a method instance shared by two layers would bind its slot config to the
+            # first layer's buffers and serve one layer's experts to another
+            logger.warning("expert-cache: %s instance is shared across layers; leaving the "
+                           "extra layers uncached", type(method).__name__)
+            declined += 1
+            continue
+        try:
+            ok = arm(module, method, logger)
+        except Exception as e:  # never break serving: the layer reads through as before
+            logger.warning("expert-cache: disabled for layer (%r)", e)
+            module._expert_cache = None
+            ok = False
+        if ok:
+            served_by.add(id(method))
+            armed.append(module._expert_cache)
+        else:
+            declined += 1
+    if not armed:
+        logger.info("expert-cache: no cacheable MoE layer found; staying out of the way")
+        return
+    c = armed[0]
+    logger.info("expert-cache %s active on %d MoE layer(s) (%d declined): %d/%d experts "
+                "resident, mirroring %s, policy=%s", _version(), len(armed), declined, c.S,
+                c.E, "+".join(c.names), settings.policy)
+
+
 def install(logger) -> bool:
-    """Wrap vLLM's post-load hook so every MoE layer is armed after weights load."""
+    """Wrap vLLM's post-load hook so that every MoE layer is armed after weights load."""
     global _installed
     if _installed:
         return True
@@ -230,55 +318,25 @@ def install(logger) -> bool:
         logger.debug("expert-cache: vLLM MoE interfaces unavailable (%r)", e)
         return False
 
-    orig = loader_utils.process_weights_after_loading
+    original = loader_utils.process_weights_after_loading
 
+    @functools.wraps(original)
     def process_weights_after_loading(model, model_config, target_device):
-        orig(model, model_config, target_device)
-        if settings.disabled:
-            return
-        armed = declined = 0
-        first = None
-        seen: set[int] = set()
-        for _, module in model.named_modules():
-            method = getattr(module, "quant_method", None)
-            if not isinstance(method, FusedMoEMethodBase):
-                continue
-            if id(method) in seen:
-                # one method instance serving two layers would bind both to one layer's
-                # slots; leave the extra layers uncached
-                logger.warning("expert-cache: %s instance is shared across layers; leaving "
-                               "the extra layers uncached", type(method).__name__)
-                declined += 1
-                continue
-            try:
-                if arm(module, method, logger):
-                    armed += 1
-                    seen.add(id(method))
-                    first = first or module._expert_cache
-                else:
-                    declined += 1
-            except Exception as e:  # never break serving: the layer reads through
-                logger.warning("expert-cache: disabled for layer (%r)", e)
-                module._expert_cache = None
-                declined += 1
-        if first is not None:
-            logger.info(
-                "expert-cache %s active on %d MoE layer(s) (%d declined): %d/%d experts "
-                "resident, mirroring %s, policy=%s", _version(), armed, declined, first.S,
-                first.E, "+".join(first.names), settings.policy)
-        else:
-            logger.info("expert-cache: no cacheable MoE layer found; staying out of the way")
+        original(model, model_config, target_device)
+        if not settings.disabled:
+            _arm_model(model, FusedMoEMethodBase, logger)
 
-    # Rebind in every module that imported the function by name (base_loader does), and
-    # at the source for importers not loaded yet.
-    patched = []
-    for name, mod in list(sys.modules.items()):
-        if mod is not None and getattr(mod, "process_weights_after_loading", None) is orig:
-            setattr(mod, "process_weights_after_loading", process_weights_after_loading)
-            patched.append(name.rsplit(".", 1)[-1])
+    # Loaders that imported the function by name (base_loader does) hold their own
+    # reference: rebind it in every loaded module that has it, and at the source for
+    # modules imported later.
+    holders = {modname: mod for modname, mod in list(sys.modules.items())
+               if mod is not None and
+               getattr(mod, "process_weights_after_loading", None) is original}
+    for mod in holders.values():
+        mod.process_weights_after_loading = process_weights_after_loading
     loader_utils.process_weights_after_loading = process_weights_after_loading
-
-    logger.info("expert-cache: hooked the MoE loader in %s", ", ".join(patched) or "utils")
+    logger.info("expert-cache: hooked the MoE loader in %s",
+                ", ".join(n.rsplit(".", 1)[-1] for n in holders) or "utils")
     _installed = True
     return True
 
