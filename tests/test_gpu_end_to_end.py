@@ -12,12 +12,14 @@ read-through path. The armed decode step is also captured in a HIP graph and rep
 """
 from __future__ import annotations
 
+import types
+
 import numpy as np
 import pytest
 import torch
 
 import gpu_util as gu
-from test_generic import Cfg, Desc, Kernel, Log
+from test_generic import new_log, quant_config
 from vllm_expert_cache.backends import generic
 
 pytestmark = pytest.mark.gpu
@@ -48,10 +50,11 @@ class TorchMoE:
 
     def __init__(self, layer):
         self.moe_quant_config = self.get_fused_moe_quant_config(layer)
-        self.moe_kernel = Kernel(self.moe_quant_config)
+        self.moe_kernel = types.SimpleNamespace(
+            fused_experts=types.SimpleNamespace(quant_config=self.moe_quant_config))
 
     def get_fused_moe_quant_config(self, layer):
-        return Cfg(Desc(), Desc(), Desc(), Desc())
+        return quant_config()
 
     def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None,
               shared_experts_input=None):
@@ -85,7 +88,7 @@ def _model(armed: bool):
              for l in range(LAYERS)]
     if armed:
         for layer, m in zip(layers, methods):
-            assert generic.arm(layer, m, Log())
+            assert generic.arm(layer, m, new_log("e2e").logger)
     return layers, methods, gates
 
 
