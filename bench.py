@@ -895,25 +895,64 @@ def _row(t, l):
     return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
 
 
+PREFETCH_RUNS = (
+    {},                                                     # no prefetch
+    {"accuracy": 1.0, "lookahead": 1, "one_launch": False, "late_fork": False},
+    {"accuracy": 1.0, "lookahead": 1, "one_launch": True, "late_fork": False},
+    {"accuracy": 1.0, "lookahead": 1},
+    {"accuracy": 1.0, "lookahead": 2},
+    {"accuracy": 0.8, "lookahead": 1, "late_fork": False},
+    {"accuracy": 0.8, "lookahead": 1},
+    {"accuracy": 0.8, "lookahead": 2},
+    {"accuracy": 0.8, "lookahead": 1, "budget": 1},
+    {"accuracy": 0.8, "lookahead": 1, "errors": "routed"},
+    {"accuracy": 0.8, "lookahead": 2, "errors": "routed"},
+)
+
+
+def _predictions(np, ids_np, W, K, E, q, errors):
+    """The true routing of steps W..W+K with each id replaced, with probability 1 - q, by a
+    wrong guess: a uniformly random expert ("uniform"), or an expert the same layer routes
+    at a random step of the trace ("routed": a plausible alternative, drawn as often as the
+    layer routes it)."""
+    rng = np.random.default_rng(int(q * 1000) + (1 if errors == "routed" else 0))
+    pred = ids_np[W:W + K].copy()
+    wrong = (rng.random(pred.shape) >= q) & (pred >= 0)
+    n = int(wrong.sum())
+    if errors == "uniform":
+        pred[wrong] = rng.integers(0, E, n)
+    else:
+        layer = np.nonzero(wrong)[1]
+        pred[wrong] = ids_np[rng.integers(0, ids_np.shape[0], n), layer,
+                             rng.integers(0, ids_np.shape[2], n)]
+    return pred
+
+
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
-                 W, T, B_exp, chunks, lanes, dev, peak, window=1024, compute=(0, 50),
-                 configs=((None, 0, False, None), (1.0, 1, False, None), (1.0, 1, True, None),
-                          (0.8, 1, True, None), (0.8, 1, True, 1), (1.0, 2, True, None),
-                          (1.0, 4, True, None))):
+                 W, T, B_exp, chunks, lanes, dev, peak, window=1024,
+                 compute=(0, 50), runs=PREFETCH_RUNS):
     """Prefetch over trace steps W..T, every run from the same start state (the snapshot
-    `snap` taken at step W of the trace pass), as one captured graph per decode step. With a lookahead of d layers:
+    `snap` taken at step W of the trace pass), as one captured graph per decode step.
+
+    With a lookahead of d layers:
       d = 0 (no prefetch): per layer l, manage+remap(l), gather(l), compute(l);
       d >= 1: layers 0..d-1 prefetched first, then per layer l the prefetch step of layer
               l+d and manage+remap(l) -- two launches (expert_cache_prefetch, then
               expert_cache_manage_remap) or one (expert_cache_manage_remap_prefetch) --,
-              the copy of the prefetched experts forked onto a side stream, a wait for
-              layer l's prefetch copy, gather(l) of what is still missing, compute(l).
+              a wait for layer l's prefetch copy, gather(l) of what is still missing,
+              compute(l). The copy of layer l+d's prefetched experts
+              (expert_cache_gather_live, on a side stream) forks right after the policy
+              launch ("late_fork": False) or after gather(l) (the default), so that it
+              overlaps compute(l) instead of sharing the host link with gather(l).
+    The real step of a layer settles its pending prefetch installs: routed ones stay, the
+    others are dropped, and their live copy stops.
+
     compute(l) stands in for the layer's attention and expert GEMMs: a spin of C us on one
-    CU (C = 0: no compute, so prefetch has nothing to hide behind). The predictor is the true
-    routing with each id replaced, with probability 1 - accuracy, by a random expert;
-    accuracy 1.0 is an upper bound no real predictor reaches. `configs` lists (accuracy,
-    lookahead, one launch, insert budget per prefetch step or None for S); (None, 0, False,
-    None) is the run without prefetch."""
+    CU (C = 0: no compute, so prefetch has nothing to hide behind). Predictions come from
+    _predictions; accuracy 1.0 is an upper bound no real predictor reaches. Each run is a
+    dict of accuracy (absent: no prefetch), lookahead, one_launch (default True), late_fork
+    (default True), budget (inserts per prefetch step, default S) and errors ("uniform",
+    the default, or "routed")."""
     K = min(window, T - W)
     i32 = torch.int32
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
@@ -951,19 +990,20 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     p_args = [(_row(pred_static, l), mk, E, S, S, st.row("table", l), st.row("map_cold", l),
                st.row("slot_expert", l), st.row("slot_stamp", l), st.row("routed", l),
                _row(pf_miss, l), _row(pf_nm, l)) for l in range(L)]
-    gp_args = [tuple(g_args[l][:18]) + (_row(pf_miss, l), _row(pf_nm, l), chunks, lanes)
+    gp_args = [tuple(g_args[l][:18]) + (_row(pf_miss, l), _row(pf_nm, l),
+                                        st.row("slot_expert", l), chunks, lanes)
                for l in range(L)]
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
 
-    def launch(cur, la, one, budget, spin):
+    def launch(cur, la, one, late, budget, spin):
         c = ctypes.c_void_p(cur.cuda_stream)
         sd = ctypes.c_void_p(side.cuda_stream)
         pa = [a[:4] + (budget,) + a[5:] for a in p_args]
 
         def copy(l):
             side.wait_stream(cur)
-            rc = lib.expert_cache_gather(*gp_args[l], sd)
+            rc = lib.expert_cache_gather_live(*gp_args[l], sd)
             done[l].record(side)
             return rc
 
@@ -972,18 +1012,28 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             rc |= lib.expert_cache_prefetch(*pa[j], c) | copy(j)
         for l in range(L):
             n = l + la
+            fork = None
             if la and n < L and one:
                 rc |= lib.expert_cache_manage_remap_prefetch(*m_args[l], _row(pred_static, n),
                                                              mk, budget, *pa[n][5:], c)
-                rc |= copy(n)
+                fork = n
             elif la and n < L:
-                rc |= lib.expert_cache_prefetch(*pa[n], c) | copy(n)
+                rc |= lib.expert_cache_prefetch(*pa[n], c)
+                fork = n
+                if not late:
+                    rc |= copy(n)
+                    fork = None
                 rc |= lib.expert_cache_manage_remap(*m_args[l], c)
             else:
                 rc |= lib.expert_cache_manage_remap(*m_args[l], c)
+            if fork is not None and not late:
+                rc |= copy(fork)
+                fork = None
             if la:
                 cur.wait_event(done[l])
             rc |= lib.expert_cache_gather(*gr_args[l], c)
+            if fork is not None:
+                rc |= copy(fork)
             if spin:
                 torch.cuda._sleep(spin)
         if rc:
@@ -992,24 +1042,23 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     out = []
     base_ms = {}
     for C in compute:
-        for q, la, one, budget in configs:
-            budget = S if budget is None else budget
-            if q is None:
-                pred = None
-            else:
-                rng = np.random.default_rng(int(q * 1000))
-                pred = ids_np[W:W + K].copy()
-                if q < 1.0:
-                    wrong = (rng.random(pred.shape) >= q) & (pred >= 0)
-                    pred[wrong] = rng.integers(0, E, int(wrong.sum()))
-                pred_dev = torch.as_tensor(pred, device=dev)
+        for run in runs:
+            q = run.get("accuracy")
+            la = run.get("lookahead", 0) if q is not None else 0
+            one, late = run.get("one_launch", True), run.get("late_fork", True)
+            budget = run.get("budget") or S
+            errors = run.get("errors", "uniform")
+            pred = None if q is None else (ids_np[W:W + K].copy() if q >= 1.0 else
+                                           _predictions(np, ids_np, W, K, E, q, errors))
+            if pred is not None:
+                pred_dev = torch.as_tensor(np.ascontiguousarray(pred), device=dev)
             st.restore(snap)
             pf_nm.zero_()
             pf_hist.zero_()
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream(), la, one, budget, int(C * cyc_per_us))
+                launch(torch.cuda.current_stream(), la, one, late, budget, int(C * cyc_per_us))
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             a.record()
@@ -1033,30 +1082,37 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 valid = np.arange(S)[None, None, :] < pn[..., None]
                 used = int((routed[tt[..., None], ll[..., None], np.where(valid, fetched, 0)]
                             & valid).sum())
-            moved = int(nm.sum() + pn.sum())
             ms = 1e3 * elapsed / K
             if q is None:
                 base_ms[C] = ms
-            gbps = moved * B_exp / elapsed / 1e9
+            useful = (int(nm.sum()) + used) * B_exp / elapsed / 1e9
             out.append({"compute_us_per_layer": C, "predictor_accuracy": q,
-                        "lookahead_layers": la, "one_launch": one,
+                        "prediction_errors": errors if q is not None and q < 1.0 else None,
+                        "lookahead_layers": la, "one_launch": one if la else None,
+                        "copy_fork": (None if not la else
+                                      "after the layer's gather" if late else
+                                      "after the policy launch"),
                         "insert_budget": budget if q is not None else None,
                         "ms_per_step": round(ms, 4),
                         "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
-                        "moved_GBps": round(gbps, 3),
-                        "moved_frac_of_link_peak": round(gbps / peak, 4),
+                        "useful_GBps": round(useful, 3),
                         "prefetch_inserts": int(pn.sum()), "prefetch_used": used,
+                        "prefetch_dropped": int(pn.sum()) - used,
                         "critical_path_inserts": int(nm.sum()),
                         "real_step_hit_rate": round(1.0 - float(nm.sum()) / distinct, 5)})
-            capped = f", budget {budget}" if q is not None and budget < S else ""
-            log(f"prefetch leg, compute {C} us/layer, predictor "
-                f"{'none' if q is None else q}, lookahead {la}"
-                f"{', one launch' if one else ''}{capped}: {ms:.3f} ms/step "
-                f"({base_ms[C] / ms:.3f}x), {moved} experts moved at {gbps:.2f} GB/s, "
-                f"{int(pn.sum())} prefetched ({used} used), {int(nm.sum())} on the critical "
-                f"path")
-    return {"window_steps": K, "timed_trace_steps": [W, W + K],
-            "spin_cycles_per_us": round(cyc_per_us, 1), "runs": out}
+            desc = "none" if q is None else (
+                f"{q} ({errors} errors), lookahead {la}"
+                f"{', one launch' if one else ', two launches'}"
+                f"{', copy forked after the gather' if late else ''}"
+                f"{f', budget {budget}' if budget < S else ''}")
+            log(f"prefetch leg, compute {C} us/layer, predictor {desc}: {ms:.3f} ms/step "
+                f"({base_ms[C] / ms:.3f}x), {int(pn.sum())} prefetched ({used} used), "
+                f"{int(nm.sum())} on the critical path")
+    return {"window_steps": K, "trace_steps": [W, W + K],
+            "spin_cycles_per_us": round(cyc_per_us, 1),
+            "def": "useful_GBps counts the experts a step needed (critical-path inserts plus "
+                   "prefetched experts that were routed), not the partial copies of dropped "
+                   "predictions", "runs": out}
 
 
 def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):

@@ -62,6 +62,26 @@ int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void*
                         hipStream_t stream);
 
 /*
+ * expert_cache_gather for the miss list of a prefetch step (expert_cache_prefetch), which
+ * may run while the real step that settles those installs runs on another stream: a tile of
+ * pair (e, slot) is loaded only while slot_expert[slot] == e, so once the real step drops a
+ * prediction its copy stops within a tile or two per workgroup. The comparison reads
+ * slot_expert with device-coherent loads; the first tile of each pair is loaded without
+ * one. Tiles already loaded are stored. Confirmed and still-pending predictions are copied
+ * whole. The caller must order any later copy into these slots (the real step's gather)
+ * after this call, as it must for any prefetch copy.
+ * Fails with -1 where expert_cache_gather does, or when slot_expert is null.
+ *
+ * No counterpart in the reference's C-ABI (prefetch is README.md:392-394's next step).
+ */
+int expert_cache_gather_live(void* d0, const void* s0, long b0, void* d1, const void* s1,
+                             long b1, void* d2, const void* s2, long b2, void* d3,
+                             const void* s3, long b3, void* d4, const void* s4, long b4,
+                             void* d5, const void* s5, long b5, const int* miss,
+                             const int* n_miss, const int* slot_expert, int chunks, int lanes,
+                             hipStream_t stream);
+
+/*
  * The LRU policy step (hits and installs stamp the current step, no decay) followed by both
  * moe_align_block_size outputs built from the updated table: the resident side bucketed by
  * slot, the non-resident side bucketed by expert id; sentinel mk in sorted_*, -1 in unused
@@ -116,11 +136,19 @@ int expert_cache_manage_remap(const void* ids, int id_bytes, int mk, int E, int 
  * among the slots whose expert is not predicted, at most max_inserts of them, writing the
  * (expert, slot) pairs to miss and their count to n_miss -- but it does not advance any step
  * counter, leaves the stamps of resident predicted experts alone, never ages, and gives each
- * install stamp 0. An unused prediction is therefore the first victim of the next real step,
- * and a right prediction leaves the policy state after the next expert_cache_manage equal to
- * what that call alone would give (except on an LFU step that would have aged the counts).
+ * install stamp -1, marking it pending. The next served call of expert_cache_manage (or of
+ * the manage_remap / fused entry points) settles every pending slot before counting hits:
+ * one whose expert is routed is confirmed and ends that step with the stamp a real install
+ * of the step gets (the step number under LRU, 1 under LFU, after any ageing); one whose
+ * expert is not routed is dropped -- table[e] = -1, map_cold[e] = e, the slot empty at stamp
+ * 0 -- so a wrong prediction leaves nothing resident behind. A right prediction leaves the
+ * policy state after the next expert_cache_manage equal to what that call alone would give
+ * (except on an LFU step that would have aged the counts). Pending keys sort below every
+ * real key, so a further prefetch step evicts unconfirmed predictions first. The
+ * reference's states never hold a negative stamp, so on them nothing here changes.
  * `routed` is left holding the predicted flags. pred_ids are int32; ids outside [0, E) are
- * ignored. Use a miss/n_miss pair of its own, not the one the real step's gather reads.
+ * ignored. Use a miss/n_miss pair of its own, not the one the real step's gather reads, and
+ * copy with expert_cache_gather_live so that dropped predictions stop copying.
  * Fails with -1 unless E > 0, 0 < S <= 1024, 0 <= max_inserts <= 1024 and mk >= 0.
  *
  * No counterpart in the reference's C-ABI: README.md:392-394 names next-layer prefetch as

@@ -64,11 +64,23 @@ static inline int slot_evictable(const int32_t* slot_expert, const uint8_t* rout
 /* Front half shared by both victim rules: steps 1-6 of one manage call.
  * Returns the number of inserts to attempt (nins), or -1 when the call stops early
  * (read-through or nothing to insert). `misses` receives the missing experts in ascending
- * id order (at most nins of them). */
+ * id order (at most nins of them).
+ *
+ * Pending prefetch installs. A slot whose stamp is negative holds an expert that
+ * oracle_prefetch installed and no real step has seen since (the reference never produces a
+ * negative stamp, so on its states nothing below changes). Once the step is served (past the
+ * read-through check), each such slot is settled before hits are counted:
+ *   - its expert is routed: the prediction is confirmed, and the slot ends the step with the
+ *     stamp a real install of this step gets (st under LRU, 1 under LFU; after any ageing),
+ *     instead of a hit's refresh;
+ *   - its expert is not routed: the prediction is dropped, as if it had never been copied
+ *     (its copy may be cut short): table = -1 and map_cold = itself for the expert, the slot
+ *     becomes empty with stamp 0 and is evictable like any other empty slot. */
 static int manage_front(const int32_t* ids, int mk, int E, int S, int max_distinct,
-                        int max_inserts, int32_t* table, int64_t* slot_stamp,
-                        uint8_t* routed, int64_t* step, int32_t* miss, int32_t* n_miss,
-                        int policy, int decay, int32_t* misses, int64_t* st_out) {
+                        int max_inserts, int32_t* table, int32_t* map_cold,
+                        int32_t* slot_expert, int64_t* slot_stamp, uint8_t* routed,
+                        int64_t* step, int32_t* miss, int32_t* n_miss, int policy, int decay,
+                        int32_t* misses, int64_t* st_out) {
   /* step advances and n_miss clears on every call (kernels/expert_cache.hip:214-217) */
   step[0] += 1;
   n_miss[0] = 0;
@@ -85,13 +97,31 @@ static int manage_front(const int32_t* ids, int mk, int E, int S, int max_distin
   for (int e = 0; e < E; e++) cnt += routed[e];
   if (cnt > max_distinct) return -1; /* read-through: nothing else changes (:228-232) */
 
+  /* settle pending prefetch installs (see above) */
+  const int64_t fresh = (policy == 0) ? st : 1;
+  uint8_t confirmed[OR_MAXS];
+  for (int i = 0; i < S; i++) {
+    const int x = slot_expert[i];
+    confirmed[i] = 0;
+    if (slot_stamp[i] >= 0 || x < 0 || x >= E) continue;
+    if (routed[x]) {
+      confirmed[i] = 1;
+    } else {
+      table[x] = -1;
+      map_cold[x] = x;
+      slot_expert[i] = -1;
+      slot_stamp[i] = 0;
+    }
+  }
+
   /* hits refresh, misses enumerate in ascending id (:234-246; test_policy.py:97-106) */
   int total = 0;
   for (int e = 0; e < E; e++) {
     if (!routed[e]) continue;
     const int s = table[e];
     if (s >= 0) {
-      if (s < S) slot_stamp[s] = (policy == 0) ? st : (int64_t)((uint64_t)slot_stamp[s] + 1);
+      if (s < S && !confirmed[s])
+        slot_stamp[s] = (policy == 0) ? st : (int64_t)((uint64_t)slot_stamp[s] + 1);
     } else {
       if (total < max_inserts) misses[total] = e;
       total++;
@@ -99,12 +129,14 @@ static int manage_front(const int32_t* ids, int mk, int E, int S, int max_distin
   }
   const int nins = total < max_inserts ? total : max_inserts;
   for (int j = 0; j < nins; j++) miss[2 * j] = misses[j]; /* even if fewer install (:252-259) */
-  if (nins == 0) return -1; /* no decay on a step without inserts (:251) */
 
-  /* LFU ageing: halve every stamp on steps where st % decay == 0 (:261-267) */
-  if (policy != 0 && decay > 0 && (st % (int64_t)decay) == 0)
+  /* LFU ageing: halve every stamp on inserting steps where st % decay == 0 (:261-267); no
+   * decay on a step without inserts (:251) */
+  if (nins > 0 && policy != 0 && decay > 0 && (st % (int64_t)decay) == 0)
     for (int i = 0; i < S; i++) slot_stamp[i] >>= 1;
-  return nins;
+  for (int i = 0; i < S; i++)
+    if (confirmed[i]) slot_stamp[i] = fresh;
+  return nins > 0 ? nins : -1;
 }
 
 /* installVictim (kernels/expert_cache.hip:104-121; test_policy.py:122-131) */
@@ -133,8 +165,9 @@ int oracle_manage_serial(const int32_t* ids, int mk, int E, int S, int max_disti
   if (manage_args_bad(E, S, max_inserts, policy)) return -1;
   int32_t misses[OR_MAXINS];
   int64_t st;
-  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, slot_stamp,
-                                routed, step, miss, n_miss, policy, decay, misses, &st);
+  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
+                                decay, misses, &st);
   if (nins < 0) return 0;
   const int64_t fresh = (policy == 0) ? st : 1;
   int nact = 0;
@@ -163,8 +196,9 @@ int oracle_manage_rank(const int32_t* ids, int mk, int E, int S, int max_distinc
   if (manage_args_bad(E, S, max_inserts, policy)) return -1;
   int32_t misses[OR_MAXINS];
   int64_t st;
-  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, slot_stamp,
-                                routed, step, miss, n_miss, policy, decay, misses, &st);
+  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                slot_expert, slot_stamp, routed, step, miss, n_miss, policy,
+                                decay, misses, &st);
   if (nins < 0) return 0;
   const int64_t fresh = (policy == 0) ? st : 1;
   int64_t key[OR_MAXS];
@@ -198,13 +232,15 @@ int oracle_manage_rank(const int32_t* ids, int mk, int E, int S, int max_distinc
  *   - the predicted experts that are not resident, in ascending id order, are the misses;
  *     nins = min(misses, max_inserts), miss[2j] = misses[j] for j < nins;
  *   - victims are the nins smallest keys stamp<<20 | slot among the slots whose expert is not
- *     predicted, exactly as in manage; each install gets stamp 0, below every stamp a real
- *     step gives, so a wrong prediction is the first victim afterwards, and a right one's
- *     first real hit gives it the stamp a real install would have (st under LRU, 1 under
- *     LFU).
+ *     predicted, exactly as in manage; each install gets stamp -1, which marks it pending:
+ *     the next served manage step confirms it if its expert is routed (the slot takes the
+ *     stamp a real install of that step gets) and drops it otherwise (the slot is emptied),
+ *     see manage_front. A pending slot's key is below every real key, so a later prefetch
+ *     step evicts unconfirmed predictions first.
  * Consequence, checked by the tests: with the prediction equal to the next step's routed set,
  * prefetch followed by manage leaves the same state as manage alone, with the miss list
- * moved to the prefetch, whenever that manage step would not decay.
+ * moved to the prefetch, whenever that manage step would not decay. A wrong prediction
+ * leaves no expert behind: the step that drops it empties its slot.
  * `rule` 0 = serial argmin, 1 = rank.
  * ------------------------------------------------------------------------------------- */
 int oracle_prefetch(const int32_t* ids, int mk, int E, int S, int max_inserts, int32_t* table,
@@ -239,7 +275,7 @@ int oracle_prefetch(const int32_t* ids, int mk, int E, int S, int max_inserts, i
           best = i;
       }
       if (best < 0) break;
-      install(r, best, misses[r], 0, E, table, map_cold, slot_expert, slot_stamp, miss);
+      install(r, best, misses[r], -1, E, table, map_cold, slot_expert, slot_stamp, miss);
       nact++;
     }
   } else {
@@ -260,7 +296,7 @@ int oracle_prefetch(const int32_t* ids, int mk, int E, int S, int max_inserts, i
     }
     nact = nins < nev ? nins : nev;
     for (int r = 0; r < nact; r++)
-      install(r, vic[r], misses[r], 0, E, table, map_cold, slot_expert, slot_stamp, miss);
+      install(r, vic[r], misses[r], -1, E, table, map_cold, slot_expert, slot_stamp, miss);
   }
   n_miss[0] = nact;
   return 0;
@@ -401,8 +437,9 @@ int oracle_fused(const int32_t* ids, int mk, int E, int S, int max_distinct, int
   /* manage half: the rank rule with policy 0 and no decay */
   int32_t misses[OR_MAXE_FUSED];
   int64_t st;
-  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, slot_stamp,
-                                routed, step, miss, n_miss, 0, 0, misses, &st);
+  const int nins = manage_front(ids, mk, E, S, max_distinct, max_inserts, table, map_cold,
+                                slot_expert, slot_stamp, routed, step, miss, n_miss, 0, 0,
+                                misses, &st);
   if (nins > 0) {
     int64_t key[OR_MAXS];
     uint8_t ev[OR_MAXS];

@@ -102,6 +102,19 @@ def test_gather_rejects_like_reference(lib, ref, sizes, chunks, lanes):
     assert _gather(ref, sizes, chunks, lanes) == -1
 
 
+@pytest.mark.parametrize("sizes,chunks,lanes", BAD_GATHER)
+def test_gather_live_rejects_what_gather_rejects(lib, sizes, chunks, lanes):
+    args = []
+    for b in sizes:
+        args += [P(1), P(1), ctypes.c_long(b)]
+    assert lib.expert_cache_gather_live(*args, P(1), P(1), P(1), chunks, lanes, None) == -1
+
+
+def test_gather_live_rejects_a_null_slot_table(lib):
+    args = [P(1), P(1), ctypes.c_long(16)] * 6
+    assert lib.expert_cache_gather_live(*args, P(1), P(1), None, 32, 1, None) == -1
+
+
 def _fused(h, E, S, mi, bs, L, NB, mk=1):
     fn = h.expert_cache_fused
     fn.restype = ctypes.c_int

@@ -196,3 +196,67 @@ def test_gather_on_the_reference_suite_shape(chunks, lanes):
     for sl, e in written.items():
         assert se[sl] == e
         store.check_slot(sl, e)
+
+
+def _live_call(store: Expertstore, miss, n_miss, slot_expert, chunks=32, lanes=1):
+    return gu.lib().expert_cache_gather_live(*store.gather_args(), gu.ptr(miss),
+                                             gu.ptr(n_miss), gu.ptr(slot_expert), chunks,
+                                             lanes, gu.stream())
+
+
+@pytest.mark.parametrize("chunks,lanes", [(1, 1), (3, 7), (32, 1), (64, 64)])
+def test_gather_live_copies_live_pairs_like_gather(chunks, lanes):
+    """expert_cache_gather_live with every pair live (slot_expert names each pair's expert):
+    the same bytes as expert_cache_gather, and nothing outside the listed slots changes."""
+    store = Expertstore(24, 10, ODD_SIZES, seed=7)
+    for d in store.dst:
+        d.fill_(0x5A)
+    pairs = [(3, 0), (17, 4), (9, 7), (22, 9)]
+    miss = torch.tensor([v for p in pairs for v in p], dtype=torch.int32, device=gu.DEV)
+    n_miss = torch.tensor([len(pairs)], dtype=torch.int32, device=gu.DEV)
+    slot_expert = torch.full((10,), -1, dtype=torch.int32, device=gu.DEV)
+    for e, sl in pairs:
+        slot_expert[sl] = e
+    assert _live_call(store, miss, n_miss, slot_expert, chunks, lanes) == 0
+    torch.cuda.synchronize()
+    for e, sl in pairs:
+        store.check_slot(sl, e)
+    listed = {sl for _, sl in pairs}
+    for i, b in enumerate(store.sizes):
+        for sl in range(10):
+            if sl not in listed:
+                assert bool((store.dst[i][sl * b:(sl + 1) * b] == 0x5A).all())
+
+
+def test_gather_live_stops_loading_dropped_pairs():
+    """Pairs whose slot no longer names their expert (dropped, or given another expert)
+    before the launch: each workgroup loads at most the first tile it meets of such a pair,
+    so a 4.7 MB expert moves at most 32 workgroups x one 8 KB tile, and what lands is whole
+    tiles of the right source bytes, the rest of the slot untouched. Live pairs in the same
+    list are copied whole."""
+    w = traces.WORKLOADS["48-layer-e128"]
+    sizes = [b.nbytes for b in w.buffers]
+    store = Expertstore(12, 6, sizes, seed=9)
+    for d in store.dst:
+        d.fill_(0x5A)
+    pairs = [(2, 0), (5, 1), (7, 2), (11, 3)]
+    miss = torch.tensor([v for p in pairs for v in p], dtype=torch.int32, device=gu.DEV)
+    n_miss = torch.tensor([4], dtype=torch.int32, device=gu.DEV)
+    slot_expert = torch.tensor([2, -1, 9, 11, -1, -1], dtype=torch.int32, device=gu.DEV)
+    assert _live_call(store, miss, n_miss, slot_expert) == 0
+    torch.cuda.synchronize()
+    store.check_slot(0, 2)
+    store.check_slot(3, 11)
+    tile = 256 * 2 * 16
+    for e, sl in ((5, 1), (7, 2)):
+        copied = 0
+        for i, b in enumerate(sizes):
+            got = store.dst[i][sl * b:(sl + 1) * b]
+            want = store.host[i][e * b:(e + 1) * b].to(gu.DEV)
+            for t0 in range(0, b, tile):
+                g, wv = got[t0:t0 + tile], want[t0:t0 + tile]
+                if torch.equal(g, wv):
+                    copied += 1
+                else:
+                    assert bool((g == 0x5A).all()), (e, i, t0)  # untouched, never partial
+        assert copied <= 32, (e, copied)

@@ -249,8 +249,11 @@ def test_cache_prefetch_under_graph_capture():
         for f in ("table", "map_cold", "slot_expert", "slot_stamp", "step", "pf_miss",
                   "pf_n_miss", "miss", "n_miss"):
             assert torch.equal(getattr(graphed, f), getattr(eager, f)), (t, f)
+        # resident slots only: a dropped prediction's slot is empty, and how much of it the
+        # live copy wrote before stopping depends on timing
+        live = graphed.slot_expert >= 0
         for n in NAMES:
-            assert torch.equal(graphed.slots[n], eager.slots[n]), (t, n)
+            assert torch.equal(graphed.slots[n][live], eager.slots[n][live]), (t, n)
         _all_slots_hold_their_experts(graphed, src)
 
 

@@ -30,6 +30,42 @@ bool ranges_meet(const void* p, long long pn, const void* q, long long qn) {
   return pn > 0 && qn > 0 && a < b + qn && b < a + pn;
 }
 
+// The gather's launch arguments from the six (dst, src, bytes) triples: the checks of
+// kernels/expert_cache.hip:631-634, then the buffers with a repeated (dst, src, bytes) -- the
+// caller's padding of a short list -- dropped, since they would copy the same bytes to the
+// same place, and each workgroup's stride through the step's (miss, tile) space.
+bool gather_plan(void* const (&dst)[kGatherBufs], const void* const (&src)[kGatherBufs],
+                 const long (&bytes)[kGatherBufs], int chunks, int lanes, GatherArgs& g) {
+  for (int i = 0; i < kGatherBufs; i++)
+    if (bytes[i] <= 0 || bytes[i] % 16) return false;
+  if (chunks <= 0 || lanes <= 0) return false;
+  constexpr long long kTile = (long long)kGatherThreads * kGatherUnroll;
+  g.nbuf = 0;
+  g.tile0[0] = 0;
+  for (int i = 0; i < kGatherBufs; i++) {
+    bool dup = false;
+    for (int k = 0; k < i; k++)
+      dup = dup || (dst[k] == dst[i] && src[k] == src[i] && bytes[k] == bytes[i]);
+    if (dup) continue;
+    const int b = g.nbuf++;
+    g.dst[b] = static_cast<u32x4*>(dst[i]);
+    g.src[b] = static_cast<const u32x4*>(src[i]);
+    g.vec[b] = bytes[i] / 16;
+    g.tile0[b + 1] = g.tile0[b] + (g.vec[b] + kTile - 1) / kTile;
+  }
+  for (int b = g.nbuf; b < kGatherBufs; b++) {
+    g.dst[b] = nullptr;
+    g.src[b] = nullptr;
+    g.vec[b] = 0;
+    g.tile0[b + 1] = g.tile0[b];
+  }
+  g.per = g.tile0[g.nbuf];
+  const long long nblk = (long long)chunks * lanes;
+  g.jstep = g.per > 0 ? nblk / g.per : 0;
+  g.rstep = g.per > 0 ? nblk % g.per : 0;
+  return true;
+}
+
 bool manage_args_bad(int E, int S, int max_inserts, int policy) {
   if (E <= 0 || S <= 0 || S > kMaxSlots || S > kSlotMask) return true;
   if (max_inserts < 0 || max_inserts > kMaxInserts) return true;
@@ -299,39 +335,26 @@ int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void*
   void* const dst[kGatherBufs] = {d0, d1, d2, d3, d4, d5};
   const void* const src[kGatherBufs] = {s0, s1, s2, s3, s4, s5};
   const long bytes[kGatherBufs] = {b0, b1, b2, b3, b4, b5};
-  for (int i = 0; i < kGatherBufs; i++)
-    if (bytes[i] <= 0 || bytes[i] % 16) return -1;
-  if (chunks <= 0 || lanes <= 0) return -1;
-
-  // A buffer passed again with the same (dst, src, bytes) -- the caller's padding of a
-  // short buffer list -- would copy the same bytes to the same place; copy it once.
-  constexpr long long kTile = (long long)kGatherThreads * kGatherUnroll;
   GatherArgs g;
-  g.nbuf = 0;
-  g.tile0[0] = 0;
-  for (int i = 0; i < kGatherBufs; i++) {
-    bool dup = false;
-    for (int k = 0; k < i; k++)
-      dup = dup || (dst[k] == dst[i] && src[k] == src[i] && bytes[k] == bytes[i]);
-    if (dup) continue;
-    const int b = g.nbuf++;
-    g.dst[b] = static_cast<u32x4*>(dst[i]);
-    g.src[b] = static_cast<const u32x4*>(src[i]);
-    g.vec[b] = bytes[i] / 16;
-    g.tile0[b + 1] = g.tile0[b] + (g.vec[b] + kTile - 1) / kTile;
-  }
-  for (int b = g.nbuf; b < kGatherBufs; b++) {
-    g.dst[b] = nullptr;
-    g.src[b] = nullptr;
-    g.vec[b] = 0;
-    g.tile0[b + 1] = g.tile0[b];
-  }
-  g.per = g.tile0[g.nbuf];
-  const long long nblk = (long long)chunks * lanes;
-  g.jstep = g.per > 0 ? nblk / g.per : 0;
-  g.rstep = g.per > 0 ? nblk % g.per : 0;
-  hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false>), dim3(chunks, lanes),
-                     dim3(kGatherThreads), 0, stream, g, miss, n_miss);
+  if (!gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
+  hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false, false>), dim3(chunks, lanes),
+                     dim3(kGatherThreads), 0, stream, g, miss, n_miss, nullptr);
+  return (int)hipGetLastError();
+}
+
+int expert_cache_gather_live(void* d0, const void* s0, long b0, void* d1, const void* s1,
+                             long b1, void* d2, const void* s2, long b2, void* d3,
+                             const void* s3, long b3, void* d4, const void* s4, long b4,
+                             void* d5, const void* s5, long b5, const int* miss,
+                             const int* n_miss, const int* slot_expert, int chunks, int lanes,
+                             hipStream_t stream) {
+  void* const dst[kGatherBufs] = {d0, d1, d2, d3, d4, d5};
+  const void* const src[kGatherBufs] = {s0, s1, s2, s3, s4, s5};
+  const long bytes[kGatherBufs] = {b0, b1, b2, b3, b4, b5};
+  GatherArgs g;
+  if (slot_expert == nullptr || !gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
+  hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false, true>), dim3(chunks, lanes),
+                     dim3(kGatherThreads), 0, stream, g, miss, n_miss, slot_expert);
   return (int)hipGetLastError();
 }
 

@@ -96,10 +96,19 @@ __device__ __forceinline__ void tile_store(const GatherTile& t, const u32x4 (&v)
 // (miss, tile-in-miss) position incrementally (no division per tile), reloads the miss pair
 // only when the walk moves to another miss, and issues the next tile's host loads before
 // storing the current tile, so the scalar bookkeeping never sits between two tiles' loads.
-template <int U, bool NT_LOAD, bool NT_STORE>
+//
+// LIVE is the copy of a prefetch step's installs, which may overlap the real step that
+// settles them: a dropped prediction's slot stops naming its expert. Before loading each
+// tile after a miss's first, the workgroup compares slot_expert[slot] with the expert and
+// stops loading that miss once they differ. The comparison uses a device-coherent load
+// issued one tile ahead, so no tile load waits for it; the first tile of a miss is loaded
+// without one. Tiles already loaded are still stored: a dropped slot is empty, or gets
+// another expert whose own copy the caller orders after this kernel.
+template <int U, bool NT_LOAD, bool NT_STORE, bool LIVE>
 __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
                                                            const int* __restrict__ miss,
-                                                           const int* __restrict__ n_miss) {
+                                                           const int* __restrict__ n_miss,
+                                                           const int* slot_expert) {
   const long long per = g.per;
   const long long t0 = (long long)blockIdx.y * gridDim.x + blockIdx.x;
   // The miss list is read only below n_miss, as kernels/expert_cache.hip:294-298 reads it:
@@ -111,9 +120,15 @@ __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
   int j = t0 < per ? 0 : (int)(t0 / per);
   long long r = t0 - (long long)j * per;
   int e = miss[2 * j], sl = miss[2 * j + 1];
+  // slot_expert[sl] as last read, for the next tile of the same miss; every such read is
+  // issued before the tile loads that follow it, so waiting for it never waits for them
+  int seen = 0;
+  if constexpr (LIVE)
+    seen = __hip_atomic_load(slot_expert + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   GatherTile cur = gather_tile<U>(g, e, sl, r);
   u32x4 v[U];
   tile_load<U, NT_LOAD>(cur, v);
+  bool have = true;  // v holds tile `cur`, to be stored
   for (;;) {
     // advance to this workgroup's next tile
     int jn = j + (int)jstep;
@@ -122,24 +137,35 @@ __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
       rn -= per;
       ++jn;
     }
-    if (jn >= nm) {
-      tile_store<U, NT_STORE>(cur, v);
-      break;
-    }
+    if (jn >= nm) break;
+    bool live = true;
     if (jn != j) {
       e = miss[2 * jn];
       sl = miss[2 * jn + 1];
+      if constexpr (LIVE)
+        seen = __hip_atomic_load(slot_expert + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if constexpr (LIVE) {
+      live = seen == e;
+      if (live)
+        seen = __hip_atomic_load(slot_expert + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     j = jn;
     r = rn;
-    const GatherTile next = gather_tile<U>(g, e, sl, r);
+    GatherTile next = cur;
     u32x4 w[U];
-    tile_load<U, NT_LOAD>(next, w);
-    tile_store<U, NT_STORE>(cur, v);
-    cur = next;
+    if (live) {
+      next = gather_tile<U>(g, e, sl, r);
+      tile_load<U, NT_LOAD>(next, w);
+    }
+    if (have) tile_store<U, NT_STORE>(cur, v);
+    have = live;
+    if (live) {
+      cur = next;
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = w[u];
+      for (int u = 0; u < U; ++u) v[u] = w[u];
+    }
   }
+  if (have) tile_store<U, NT_STORE>(cur, v);
 }
 
 }  // namespace ec

@@ -118,9 +118,15 @@ constexpr int table_chunks(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256
 //
 // PF makes it the prefetch step for predicted ids: the step counter is neither read nor
 // written, resident predicted experts keep their stamps, there is no ageing, and installs
-// get stamp 0 -- below any stamp a real step gives, so an unused prediction is the first
-// victim later and a used one gets, at its first real hit, the stamp a real install would
-// have given it (st under LRU, 1 under LFU). Victims are chosen exactly as in a real step.
+// get stamp -1, which marks them pending. Victims are chosen exactly as in a real step (a
+// pending slot's key is below every real key, so older unconfirmed predictions go first).
+//
+// A real step settles the pending slots it finds once it is served (past the read-through
+// check): a slot whose expert is routed is confirmed and ends the step with the stamp a
+// real install of this step gets (st under LRU, 1 under LFU; after any ageing); a slot
+// whose expert is not routed is dropped -- the expert leaves the table and the slot is left
+// empty at stamp 0, so a prefetch copy still in flight may stop short. The reference never
+// holds a negative stamp, so on its states none of this runs.
 template <int CS, bool GLOBAL_E, int IDB, int TQ, bool PF = false>
 __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBAL_E>& L,
                                             long long (&idv)[kIdRegs]) {
@@ -291,10 +297,12 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   const int nins = min(total, a.max_inserts);
   lds_sync();
 
-  // ---- slot side: refreshed stamps, and whether each slot's expert is routed ----------
+  // ---- slot side: refreshed stamps, whether each slot's expert is routed, and pending
+  // ---- prefetch installs confirmed or dropped -----------------------------------------
   const long long st = uniform_i64(st_v) + 1;
   const bool lru = a.policy == 0;
-  bool fx[CS];
+  const long long fresh = PF ? -1 : lru ? st : 1;
+  bool fx[CS], conf[CS];
   // all flag reads first, with clamped indexes, so they are in flight together (a
   // short-circuit test would put each read behind its own branch and wait)
   unsigned char hv[CS], fv[CS];
@@ -309,8 +317,22 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     const int x = se[c];
     const bool hit = !PF && (s < S) & (hv[c] != 0);
     fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
-    if (hit) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
-    if (nins == 0 && hit) a.slot_stamp[s] = sp[c];
+    const bool pend = !PF && (s < S) & (sp[c] < 0) & (x >= 0) & (x < E);
+    conf[c] = pend & fx[c];
+    if (pend && !fx[c]) {  // dropped: distinct slots hold distinct experts, no conflicts
+      a.table[x] = -1;
+      a.map_cold[x] = x;
+      if constexpr (!GLOBAL_E) L.tab[x] = -1;
+      se[c] = -1;
+      sp[c] = 0;
+      if (nins == 0) {
+        a.slot_expert[s] = -1;
+        a.slot_stamp[s] = 0;
+      }
+    } else if (hit || conf[c]) {
+      sp[c] = conf[c] ? fresh : lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
+      if (nins == 0) a.slot_stamp[s] = sp[c];
+    }
   }
   if (nins == 0) {  // no inserts: refreshed stamps only, no ageing
     if (lane == 0) {
@@ -320,10 +342,11 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     return;
   }
 
-  // LFU ageing on inserting steps where st % decay == 0
+  // LFU ageing on inserting steps where st % decay == 0; a confirmed slot counts as this
+  // step's install, so it takes its stamp after the halving
   if (!PF && !lru && a.decay > 0 && (st % (long long)a.decay) == 0) {
 #pragma unroll
-    for (int c = 0; c < CS; ++c) sp[c] >>= 1;
+    for (int c = 0; c < CS; ++c) sp[c] = conf[c] ? fresh : sp[c] >> 1;
   }
 
   // ---- keys of the evictable slots (expert not routed this step) ---------------------
@@ -338,7 +361,6 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     nev += __popcll(__ballot(ev[c]));
   }
   const int nact = min(nins, nev);
-  const long long fresh = PF ? 0 : lru ? st : 1;
 
   if (use_argmin<CS>(nact, nev)) {
     // ---- few inserts: repeated wave-min, each insert installed as soon as it is found.

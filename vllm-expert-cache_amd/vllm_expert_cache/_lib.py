@@ -1,11 +1,12 @@
 """ctypes binding of libexpertcache.so (C-ABI in include/expert_cache.h).
 
 Same search order and same argument lists for the reference's two bound entry points
-(vllm_expert_cache/_lib.py:15-61): manage and gather. Five more are bound here:
+(vllm_expert_cache/_lib.py:15-61): manage and gather. Six more are bound here:
 `expert_cache_fused` (exported by the reference but never bound), the two remap entry
-points that replace the reference's torch remap, `expert_cache_prefetch`, and
+points that replace the reference's torch remap, `expert_cache_prefetch`,
 `expert_cache_manage_remap_prefetch` (one layer's policy step with another's prefetch step
-in one launch). Every call is asynchronous on the caller's stream and never reads a device
+in one launch), and `expert_cache_gather_live` (the prefetch copy that stops for dropped
+predictions). Every call is asynchronous on the caller's stream and never reads a device
 value back, so the whole path is HIP-graph capturable.
 
 There is no fallback: if the library or one of its symbols is missing, loading fails with
@@ -34,6 +35,9 @@ SIGNATURES = {
     "expert_cache_manage": [_P] + [_I] * 5 + [_P] * 8 + [_I] * 2 + [_P],
     # gather(6 x (dst, src, bytes_per_expert), miss, n_miss, chunks, lanes, stream)
     "expert_cache_gather": [_P, _P, _L] * 6 + [_P, _P, _I, _I, _P],
+    # gather_live(6 x (dst, src, bytes_per_expert), miss, n_miss, slot_expert, chunks, lanes,
+    #             stream)
+    "expert_cache_gather_live": [_P, _P, _L] * 6 + [_P, _P, _P, _I, _I, _P],
     # fused(manage args without policy/decay, bs, L, NB, sorted_hot, eids_hot, npad_hot,
     #       sorted_cold, eids_cold, npad_cold, stream)
     "expert_cache_fused": [_P] + [_I] * 5 + [_P] * 8 + [_I] * 3 + [_P] * 6 + [_P],

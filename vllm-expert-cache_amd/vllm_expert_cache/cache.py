@@ -218,29 +218,32 @@ class ExpertSlotCache:
                 *own, pred.data_ptr(), int(pred.numel()), budget, *other._pf_state, stream)
         if rc != 0:
             raise RuntimeError(f"expert_cache_manage failed rc={rc}")
-        if rider is not None:
-            rider[0]._copy_prefetched()
         # a prefetched slot may be this step's victim: its copy lands before this gather
         self._wait_copy()
         self._gather(self.miss, self.n_miss, stream)
+        if rider is not None:
+            # the other layer's copy forks after this layer's gather, so it shares the host
+            # link with what follows (the expert GEMMs) rather than with this step's copy
+            rider[0]._copy_prefetched()
         return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
 
     def prefetch(self, pred_ids: torch.Tensor, max_inserts: int | None = None,
                  along: "ExpertSlotCache | None" = None) -> bool:
         """Start bringing the experts predicted for this layer's next step into slots.
 
-        The prefetch policy step (expert_cache_prefetch: installs at stamp 0, no step
+        The prefetch policy step (expert_cache_prefetch: pending installs, no step
         advance, resident predictions untouched, at most `max_inserts` installs, which
         defaults to S and is capped there) runs on the current stream. The copy of what it
-        installed runs on the device's side stream, so it overlaps whatever the current
-        stream does next. This layer's next `refresh`, or `join`, makes the current stream
-        wait for the copy. Returns False, and does nothing, when the prediction has more ids
-        than there are slots.
+        installed runs on the device's side stream (expert_cache_gather_live), so it
+        overlaps whatever the current stream does next. This layer's next `refresh` settles
+        the prediction: routed experts stay, the others are dropped and their copy stops;
+        that `refresh`, or `join`, makes the current stream wait for the copy. Returns
+        False, and does nothing, when the prediction has more ids than there are slots.
 
         With `along` (another layer's cache on the same device, with the same experts and
         slots), the policy step is staged instead: it runs inside the same launch as
-        `along`'s next policy step, at its next `refresh`, and its copy is forked from
-        there. The prediction's values are read at that launch. `along.join()`, or any
+        `along`'s next policy step, at its next `refresh`, and its copy is forked after that
+        refresh's own gather. The prediction's values are read at that launch. `along.join()`, or any
         call on this cache that reads the policy state (`refresh`, `join`, `prefetch`),
         launches a staged step on its own first."""
         ids = pred_ids if pred_ids.dtype == torch.int32 else pred_ids.to(torch.int32)
@@ -299,7 +302,9 @@ class ExpertSlotCache:
             self._pf_fork, self._pf_done = torch.cuda.Event(), torch.cuda.Event()
         self._pf_fork.record(cur)
         side.wait_event(self._pf_fork)
-        self._gather(self.pf_miss, self.pf_n_miss, side.cuda_stream)
+        # the real step that settles these installs may drop some while this copy runs: the
+        # live copy stops loading those
+        self._gather(self.pf_miss, self.pf_n_miss, side.cuda_stream, live=True)
         self._pf_done.record(side)
         self._pf_pending = True
 
@@ -314,15 +319,23 @@ class ExpertSlotCache:
             # holding the sources keeps their addresses from being reused by new tensors
             self._gather_srcs, self._gather_key = srcs, key
 
-    def _gather(self, miss: torch.Tensor, n_miss: torch.Tensor, stream) -> None:
+    def _gather(self, miss: torch.Tensor, n_miss: torch.Tensor, stream,
+                live: bool = False) -> None:
         """expert_cache_gather of every mirrored tensor over one miss list, six per call,
-        with the calls `_plan` resolved."""
+        with the calls `_plan` resolved; with `live`, expert_cache_gather_live (a prefetch
+        step's list, whose dropped predictions stop copying)."""
         h = lib()
-        tail = (miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, stream)
+        if live:
+            fn, name = h.expert_cache_gather_live, "expert_cache_gather_live"
+            tail = (miss.data_ptr(), n_miss.data_ptr(), self.slot_expert.data_ptr(),
+                    self.chunks, self.lanes, stream)
+        else:
+            fn, name = h.expert_cache_gather, "expert_cache_gather"
+            tail = (miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, stream)
         for args in self._gather_calls:
-            rc = h.expert_cache_gather(*args, *tail)
+            rc = fn(*args, *tail)
             if rc != 0:
-                raise RuntimeError(f"expert_cache_gather failed rc={rc}")
+                raise RuntimeError(f"{name} failed rc={rc}")
 
     def _gather_plan(self, srcs) -> tuple:
         """The (dst, src, bytes) x 6 argument lists of the gather calls, padded with a
