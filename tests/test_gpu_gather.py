@@ -199,9 +199,11 @@ def test_gather_on_the_reference_suite_shape(chunks, lanes):
 
 
 def _live_call(store: Expertstore, miss, n_miss, slot_expert, chunks=32, lanes=1):
-    return gu.lib().expert_cache_gather_live(*store.gather_args(), gu.ptr(miss),
-                                             gu.ptr(n_miss), gu.ptr(slot_expert), chunks,
-                                             lanes, gu.stream())
+    args = store.gather_args()
+    while len(args) < 18:  # pad to six buffers with a repeat, as cache.refresh does
+        args += args[-3:]
+    return gu.lib().expert_cache_gather_live(*args, gu.ptr(miss), gu.ptr(n_miss),
+                                             gu.ptr(slot_expert), chunks, lanes, gu.stream())
 
 
 @pytest.mark.parametrize("chunks,lanes", [(1, 1), (3, 7), (32, 1), (64, 64)])
