@@ -897,15 +897,16 @@ def _row(t, l):
 
 PREFETCH_RUNS = (
     {},                                                     # no prefetch
-    {"accuracy": 1.0, "lookahead": 1, "one_launch": False, "late_fork": False},
-    {"accuracy": 1.0, "lookahead": 1, "one_launch": True, "late_fork": False},
+    {"accuracy": 1.0, "lookahead": 1, "one_launch": False},
     {"accuracy": 1.0, "lookahead": 1},
+    {"accuracy": 1.0, "lookahead": 1, "late_fork": True},
     {"accuracy": 1.0, "lookahead": 2},
-    {"accuracy": 0.8, "lookahead": 1, "late_fork": False},
     {"accuracy": 0.8, "lookahead": 1},
+    {"accuracy": 0.8, "lookahead": 1, "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2},
     {"accuracy": 0.8, "lookahead": 1, "budget": 1},
     {"accuracy": 0.8, "lookahead": 1, "errors": "routed"},
+    {"accuracy": 0.8, "lookahead": 1, "errors": "routed", "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2, "errors": "routed"},
 )
 
@@ -942,8 +943,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
               a wait for layer l's prefetch copy, gather(l) of what is still missing,
               compute(l). The copy of layer l+d's prefetched experts
               (expert_cache_gather_live, on a side stream) forks right after the policy
-              launch ("late_fork": False) or after gather(l) (the default), so that it
-              overlaps compute(l) instead of sharing the host link with gather(l).
+              launch (the default, as ExpertSlotCache does) or, with "late_fork", after
+              gather(l), so that it does not share the host link with gather(l).
     The real step of a layer settles its pending prefetch installs: routed ones stay, the
     others are dropped, and their live copy stops.
 
@@ -951,7 +952,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     CU (C = 0: no compute, so prefetch has nothing to hide behind). Predictions come from
     _predictions; accuracy 1.0 is an upper bound no real predictor reaches. Each run is a
     dict of accuracy (absent: no prefetch), lookahead, one_launch (default True), late_fork
-    (default True), budget (inserts per prefetch step, default S) and errors ("uniform",
+    (default False), budget (inserts per prefetch step, default S) and errors ("uniform",
     the default, or "routed")."""
     K = min(window, T - W)
     i32 = torch.int32
@@ -1045,7 +1046,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
         for run in runs:
             q = run.get("accuracy")
             la = run.get("lookahead", 0) if q is not None else 0
-            one, late = run.get("one_launch", True), run.get("late_fork", True)
+            one, late = run.get("one_launch", True), run.get("late_fork", False)
             budget = run.get("budget") or S
             errors = run.get("errors", "uniform")
             pred = None if q is None else (ids_np[W:W + K].copy() if q >= 1.0 else

@@ -311,28 +311,48 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     hv[c] = L.hit[min(lane + c * kWave, S - 1)];
     fv[c] = flag[min(max(se[c], 0), E - 1)];
   }
+  bool neg = false;
+#pragma unroll
+  for (int c = 0; c < CS; ++c) {
+    const int x = se[c];
+    fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
+    conf[c] = false;
+    neg |= sp[c] < 0;
+  }
+  // Pending prefetch installs (negative stamps; none on the reference's states) are
+  // settled first, behind one wave-uniform branch: an unrouted one is dropped, a routed one
+  // confirmed by handing it to the hit refresh below at stamp 0, which yields this step's
+  // install stamp (1 under LFU, st under LRU).
+  const bool any_pending = !PF && __builtin_expect(__ballot(neg) != 0, 0);
+  if (any_pending) {
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+      const int s = lane + c * kWave;
+      const int x = se[c];
+      const bool pend = (s < S) & (sp[c] < 0) & (x >= 0) & (x < E);
+      conf[c] = pend & fx[c];
+      if (conf[c]) {
+        sp[c] = 0;
+        hv[c] = 1;
+      } else if (pend) {  // distinct slots hold distinct experts: no write conflicts
+        a.table[x] = -1;
+        a.map_cold[x] = x;
+        if constexpr (!GLOBAL_E) L.tab[x] = -1;
+        se[c] = -1;
+        sp[c] = 0;
+        if (nins == 0) {
+          a.slot_expert[s] = -1;
+          a.slot_stamp[s] = 0;
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int s = lane + c * kWave;
-    const int x = se[c];
     const bool hit = !PF && (s < S) & (hv[c] != 0);
-    fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
-    const bool pend = !PF && (s < S) & (sp[c] < 0) & (x >= 0) & (x < E);
-    conf[c] = pend & fx[c];
-    if (pend && !fx[c]) {  // dropped: distinct slots hold distinct experts, no conflicts
-      a.table[x] = -1;
-      a.map_cold[x] = x;
-      if constexpr (!GLOBAL_E) L.tab[x] = -1;
-      se[c] = -1;
-      sp[c] = 0;
-      if (nins == 0) {
-        a.slot_expert[s] = -1;
-        a.slot_stamp[s] = 0;
-      }
-    } else if (hit || conf[c]) {
-      sp[c] = conf[c] ? fresh : lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
-      if (nins == 0) a.slot_stamp[s] = sp[c];
-    }
+    if (hit) sp[c] = lru ? st : (long long)((unsigned long long)sp[c] + 1ull);
+    if (nins == 0 && hit) a.slot_stamp[s] = sp[c];
   }
   if (nins == 0) {  // no inserts: refreshed stamps only, no ageing
     if (lane == 0) {
@@ -343,10 +363,10 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   }
 
   // LFU ageing on inserting steps where st % decay == 0; a confirmed slot counts as this
-  // step's install, so it takes its stamp after the halving
+  // step's install, so it keeps its stamp through the halving
   if (!PF && !lru && a.decay > 0 && (st % (long long)a.decay) == 0) {
 #pragma unroll
-    for (int c = 0; c < CS; ++c) sp[c] = conf[c] ? fresh : sp[c] >> 1;
+    for (int c = 0; c < CS; ++c) sp[c] = conf[c] ? sp[c] : sp[c] >> 1;
   }
 
   // ---- keys of the evictable slots (expert not routed this step) ---------------------

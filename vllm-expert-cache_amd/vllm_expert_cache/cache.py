@@ -218,13 +218,14 @@ class ExpertSlotCache:
                 *own, pred.data_ptr(), int(pred.numel()), budget, *other._pf_state, stream)
         if rc != 0:
             raise RuntimeError(f"expert_cache_manage failed rc={rc}")
+        if rider is not None:
+            # forked right after the launch, the copy starts as early as it can; forked after
+            # this layer's gather it would share the link less with that gather, but a right
+            # prediction leaves that gather empty, and the later start measured slower
+            rider[0]._copy_prefetched()
         # a prefetched slot may be this step's victim: its copy lands before this gather
         self._wait_copy()
         self._gather(self.miss, self.n_miss, stream)
-        if rider is not None:
-            # the other layer's copy forks after this layer's gather, so it shares the host
-            # link with what follows (the expert GEMMs) rather than with this step's copy
-            rider[0]._copy_prefetched()
         return out if out.dtype == topk_ids.dtype else out.to(topk_ids.dtype)
 
     def prefetch(self, pred_ids: torch.Tensor, max_inserts: int | None = None,
@@ -242,8 +243,8 @@ class ExpertSlotCache:
 
         With `along` (another layer's cache on the same device, with the same experts and
         slots), the policy step is staged instead: it runs inside the same launch as
-        `along`'s next policy step, at its next `refresh`, and its copy is forked after that
-        refresh's own gather. The prediction's values are read at that launch. `along.join()`, or any
+        `along`'s next policy step, at its next `refresh`, and its copy is forked from
+        there. The prediction's values are read at that launch. `along.join()`, or any
         call on this cache that reads the policy state (`refresh`, `join`, `prefetch`),
         launches a staged step on its own first."""
         ids = pred_ids if pred_ids.dtype == torch.int32 else pred_ids.to(torch.int32)
