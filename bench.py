@@ -108,6 +108,10 @@ def parse():
     p.add_argument("--lanes", type=int, default=None)
     p.add_argument("--no-prefetch", action="store_true",
                    help="skip the next-layer prefetch leg")
+    p.add_argument("--prefetch-compute", default="0,50",
+                   help="compute stand-in per layer of the prefetch leg, us, comma-separated")
+    p.add_argument("--prefetch-steps", type=int, default=1024,
+                   help="steps per run of the prefetch leg (at most)")
     p.add_argument("--no-fused", action="store_true",
                    help="skip the expert_cache_fused leg")
     p.add_argument("--routes", default=None,
@@ -552,10 +556,12 @@ def main():
         # about 130 GB moved per run at most: 1,024 steps of the default workload, fewer
         # where experts are hundreds of MB
         per_step = max(1.0, pass_inserts * B_exp / (TP - W))
-        pw = max(32, min(1024, int(130e9 / per_step)))
+        pw = max(32, min(args.prefetch_steps, int(130e9 / per_step)))
         prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[pf0], L, E, S,
                                 mk, policy, decay, pf0, min(steps, pf0 + pw), B_exp, chunks,
-                                lanes, dev, peak)
+                                lanes, dev, peak, window=pw,
+                                compute=tuple(float(c) for c in
+                                              args.prefetch_compute.split(",")))
 
     fused = None if args.no_fused else fused_leg(torch, np, lib, dev)
 
@@ -634,7 +640,8 @@ def main():
                      "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
                                  "kernel on one 256 MB slab)",
                      "steady_state": None if late is None else {
-                         "trace_steps": [late0, TP], "segments": len(late_starts),
+                         "trace_steps": [late0, TP], "trace_inserts": int(nm[late0:TP].sum()),
+                         "segments": len(late_starts),
                          "segment_steps": late_len, "achieved": round(late["achieved"], 3),
                          "frac": round(late["achieved"] / peak, 4),
                          "achieved_launches_with_miss": rounded(late["with_miss"]),
