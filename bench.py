@@ -121,15 +121,16 @@ def parse():
     p.add_argument("--experts", type=int, default=None,
                    help="experts per layer of a --routes trace (default: the workload's)")
     p.add_argument("--traffic-probe", action="store_true",
-                   help="for rocprofv3 --pmc runs: 16 gathers of one expert each and 8 plain "
-                        "device copies of 64 MiB (the counter calibration), nothing else")
+                   help="for rocprofv3 --pmc runs: 16 gathers of one expert each (plain, then "
+                        "live), 128 policy steps and 8 plain device copies of 64 MiB (the "
+                        "counter calibration), nothing else")
     return p.parse_args()
 
 
 def traffic_probe(args):
-    """Known work for the counter runs: 16 one-expert gathers, 128 policy+remap steps of one
-    layer, and 8 plain device copies whose FETCH_SIZE / WRITE_SIZE per byte calibrate the
-    kernels' per-launch counters into bytes."""
+    """Known work for the counter runs: 16 one-expert gathers, the same 16 through the live
+    gather, 128 policy+remap steps of one layer, and 8 plain device copies whose FETCH_SIZE /
+    WRITE_SIZE per byte calibrate the kernels' per-launch counters into bytes."""
     import torch
 
     from vllm_expert_cache import _lib, traces
@@ -155,6 +156,17 @@ def traffic_probe(args):
                                      ctypes.c_void_p(one.data_ptr()), args.chunks or
                                      DEFAULT_CHUNKS, args.lanes or DEFAULT_LANES, s_ptr)
         assert rc == 0
+    # the same 16 copies through the live gather, every pair live (slot_expert names it)
+    slot_expert = torch.full((S,), -1, dtype=torch.int32, device=dev)
+    for r in range(16):
+        slot_expert.fill_(-1)
+        slot_expert[r % S] = r
+        rc = lib.expert_cache_gather_live(*a, ctypes.c_void_p(miss[r].data_ptr()),
+                                          ctypes.c_void_p(one.data_ptr()),
+                                          ctypes.c_void_p(slot_expert.data_ptr()),
+                                          args.chunks or DEFAULT_CHUNKS,
+                                          args.lanes or DEFAULT_LANES, s_ptr)
+        assert rc == 0
     # policy+remap: 128 decode steps of the workload's layer 0 from a cold start (the
     # counters of the last 64 are the steady state)
     mk = w.mk
@@ -175,7 +187,8 @@ def traffic_probe(args):
     for _ in range(8):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"gather_launches": 16, "gather_bytes_per_launch": sum(bufs),
+    print(json.dumps({"gather_launches": 16, "gather_live_launches": 16,
+                      "gather_bytes_per_launch": sum(bufs),
                       "manage_remap_launches": 128, "copy_launches": 8,
                       "copy_bytes_per_launch": n}), flush=True)
 

@@ -302,7 +302,7 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
   const long long st = uniform_i64(st_v) + 1;
   const bool lru = a.policy == 0;
   const long long fresh = PF ? -1 : lru ? st : 1;
-  bool fx[CS], conf[CS];
+  bool fx[CS];
   // all flag reads first, with clamped indexes, so they are in flight together (a
   // short-circuit test would put each read behind its own branch and wait)
   unsigned char hv[CS], fv[CS];
@@ -311,40 +311,57 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     hv[c] = L.hit[min(lane + c * kWave, S - 1)];
     fv[c] = flag[min(max(se[c], 0), E - 1)];
   }
-  bool neg = false;
+  int sign = 0;  // the OR of the stamps' high words: negative iff a stamp is
 #pragma unroll
   for (int c = 0; c < CS; ++c) {
     const int x = se[c];
     fx[c] = (x >= 0) & (x < E) & (fv[c] != 0);
-    conf[c] = false;
-    neg |= sp[c] < 0;
+    sign |= (int)((unsigned long long)sp[c] >> 32);
   }
+  const bool ageing = !PF && !lru && nins > 0 && a.decay > 0 && (st % (long long)a.decay) == 0;
   // Pending prefetch installs (negative stamps; none on the reference's states) are
-  // settled first, behind one wave-uniform branch: an unrouted one is dropped, a routed one
-  // confirmed by handing it to the hit refresh below at stamp 0, which yields this step's
-  // install stamp (1 under LFU, st under LRU).
-  const bool any_pending = !PF && __builtin_expect(__ballot(neg) != 0, 0);
-  if (any_pending) {
+  // settled first, behind one wave-uniform branch, one slot per lane and iteration through
+  // LDS so the code stays small whatever the slots per lane. An unrouted one is dropped; a
+  // routed one is handed to the hit refresh below at the stamp that makes it end the step
+  // at an install's stamp: 0 (+1 = 1 under LFU; st under LRU), or 1 when this step ages
+  // (+1, halved = 1).
+  if (!PF && __ballot(sign < 0) != 0) {
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
       const int s = lane + c * kWave;
-      const int x = se[c];
-      const bool pend = (s < S) & (sp[c] < 0) & (x >= 0) & (x < E);
-      conf[c] = pend & fx[c];
-      if (conf[c]) {
-        sp[c] = 0;
-        hv[c] = 1;
-      } else if (pend) {  // distinct slots hold distinct experts: no write conflicts
-        a.table[x] = -1;
-        a.map_cold[x] = x;
-        if constexpr (!GLOBAL_E) L.tab[x] = -1;
-        se[c] = -1;
-        sp[c] = 0;
-        if (nins == 0) {
-          a.slot_expert[s] = -1;
-          a.slot_stamp[s] = 0;
+      if (s < S) {
+        L.key[s] = sp[c];
+        L.rank[s] = se[c];
+      }
+    }
+    lds_sync();
+#pragma unroll 1
+    for (int s = lane; s < S; s += kWave) {
+      const int x = L.rank[s];
+      if (L.key[s] < 0 && x >= 0 && x < E) {
+        if (flag[x]) {
+          L.key[s] = ageing ? 1 : 0;
+          L.hit[s] = 1;
+        } else {  // distinct slots hold distinct experts: no write conflicts
+          a.table[x] = -1;
+          a.map_cold[x] = x;
+          if constexpr (!GLOBAL_E) L.tab[x] = -1;
+          L.rank[s] = -1;
+          L.key[s] = 0;
+          if (nins == 0) {
+            a.slot_expert[s] = -1;
+            a.slot_stamp[s] = 0;
+          }
         }
       }
+    }
+    lds_sync();
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+      const int s = min(lane + c * kWave, S - 1);
+      sp[c] = L.key[s];
+      se[c] = lane + c * kWave < S ? L.rank[s] : -1;
+      hv[c] = L.hit[s];
     }
   }
 #pragma unroll
@@ -362,11 +379,10 @@ __device__ __forceinline__ void manage_step(const ManageArgs& a, ManageLds<GLOBA
     return;
   }
 
-  // LFU ageing on inserting steps where st % decay == 0; a confirmed slot counts as this
-  // step's install, so it keeps its stamp through the halving
-  if (!PF && !lru && a.decay > 0 && (st % (long long)a.decay) == 0) {
+  // LFU ageing on inserting steps where st % decay == 0
+  if (ageing) {
 #pragma unroll
-    for (int c = 0; c < CS; ++c) sp[c] = conf[c] ? sp[c] : sp[c] >> 1;
+    for (int c = 0; c < CS; ++c) sp[c] >>= 1;
   }
 
   // ---- keys of the evictable slots (expert not routed this step) ---------------------
