@@ -112,6 +112,9 @@ def parse():
                    help="compute stand-in per layer of the prefetch leg, us, comma-separated")
     p.add_argument("--prefetch-steps", type=int, default=1024,
                    help="steps per run of the prefetch leg (at most)")
+    p.add_argument("--prefetch-chunks", type=int, default=None,
+                   help="workgroups of the prefetch leg's side copies (default: the "
+                        "cache's prefetch grid)")
     p.add_argument("--no-fused", action="store_true",
                    help="skip the expert_cache_fused leg")
     p.add_argument("--routes", default=None,
@@ -235,7 +238,8 @@ def main():
     import torch
 
     from vllm_expert_cache import _lib, traces
-    from vllm_expert_cache.cache import DEFAULT_CHUNKS, DEFAULT_LANES, device_address
+    from vllm_expert_cache.cache import (DEFAULT_CHUNKS, DEFAULT_LANES, PREFETCH_CHUNKS,
+                                         device_address)
 
     lib = _lib.lib()  # raises if the HIP library is missing: there is no fallback
     dev = torch.device("cuda:0")
@@ -573,6 +577,7 @@ def main():
         prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[pf0], L, E, S,
                                 mk, policy, decay, pf0, min(steps, pf0 + pw), B_exp, chunks,
                                 lanes, dev, peak, window=pw,
+                                pf_chunks=args.prefetch_chunks or PREFETCH_CHUNKS,
                                 compute=tuple(float(c) for c in
                                               args.prefetch_compute.split(",")))
 
@@ -951,7 +956,7 @@ def _predictions(np, ids_np, W, K, E, q, errors):
 
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
                  W, T, B_exp, chunks, lanes, dev, peak, window=1024,
-                 compute=(0, 50), runs=PREFETCH_RUNS):
+                 compute=(0, 50), runs=PREFETCH_RUNS, pf_chunks=None):
     """Prefetch over trace steps W..T, every run from the same start state (the snapshot
     `snap` taken at step W of the trace pass), as one captured graph per decode step.
 
@@ -1012,7 +1017,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                st.row("slot_expert", l), st.row("slot_stamp", l), st.row("routed", l),
                _row(pf_miss, l), _row(pf_nm, l)) for l in range(L)]
     gp_args = [tuple(g_args[l][:18]) + (_row(pf_miss, l), _row(pf_nm, l),
-                                        st.row("slot_expert", l), chunks, lanes)
+                                        st.row("slot_expert", l), pf_chunks or chunks, 1)
                for l in range(L)]
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
@@ -1131,6 +1136,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 f"{int(nm.sum())} on the critical path")
     return {"window_steps": K, "trace_steps": [W, W + K],
             "spin_cycles_per_us": round(cyc_per_us, 1),
+            "copy_grid": [pf_chunks or chunks, 1],
             "def": "useful_GBps counts the experts a step needed (critical-path inserts plus "
                    "prefetched experts that were routed), not the partial copies of dropped "
                    "predictions", "runs": out}

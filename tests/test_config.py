@@ -66,3 +66,24 @@ def test_entry_point_text():
     text = (Path(vllm_expert_cache.__file__).parent.parent / "pyproject.toml").read_text()
     assert '[project.entry-points."vllm.general_plugins"]' in text
     assert 'expert_cache = "vllm_expert_cache:install"' in text
+
+
+def test_gather_grids_from_the_environment(monkeypatch):
+    """The gather grid (EXPERT_CACHE_CHUNKS / _LANES, as in the reference) and the prefetch
+    copy grid (EXPERT_CACHE_PREFETCH_CHUNKS) are read when a cache is built; the defaults
+    are 32 x 1 and 16."""
+    import torch
+
+    from vllm_expert_cache.cache import ExpertSlotCache
+
+    owner = torch.nn.Module()
+    owner.w = torch.nn.Parameter(torch.zeros(8, 4), requires_grad=False)
+    for k in ("EXPERT_CACHE_CHUNKS", "EXPERT_CACHE_LANES", "EXPERT_CACHE_PREFETCH_CHUNKS"):
+        monkeypatch.delenv(k, raising=False)
+    c = ExpertSlotCache(owner, ["w"], 8, 2, "cpu")
+    assert (c.chunks, c.lanes, c.pf_chunks) == (32, 1, 16)
+    monkeypatch.setenv("EXPERT_CACHE_CHUNKS", "16")
+    monkeypatch.setenv("EXPERT_CACHE_LANES", "64")
+    monkeypatch.setenv("EXPERT_CACHE_PREFETCH_CHUNKS", "8")
+    c = ExpertSlotCache(owner, ["w"], 8, 2, "cpu")
+    assert (c.chunks, c.lanes, c.pf_chunks) == (16, 64, 8)

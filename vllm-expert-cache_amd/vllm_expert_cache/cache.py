@@ -43,6 +43,13 @@ from .config import settings
 # 4.7 MB expert, 512 reach ~41 GB/s), hence 32 x 1 rather than the reference's 16 x 64.
 DEFAULT_CHUNKS = 32
 DEFAULT_LANES = 1
+# Prefetch copies run beside the decode chain on another stream. The host link is shared
+# with the command processor's own reads, so the more a copy keeps in flight, the longer
+# every dispatch of the chain waits (measured on MI355X, a dependent 48-layer chain beside a
+# streaming copy: +2.4 us per layer at 4 workgroups, +6.7 at 16, +17.5 at 32, +110 at 64,
+# while the copy itself reaches 20, 56.7, 57.5 and 56.1 GB/s). 16 workgroups still fill the
+# link; in the prefetch pipeline they beat 12, 20, 24 and 32 for every predictor measured.
+PREFETCH_CHUNKS = 16
 
 # One side stream per device carries every layer's prefetch copy: the copies share one host
 # link, so running them one after another loses nothing. Default priority.
@@ -164,6 +171,8 @@ class ExpertSlotCache:
         self.decay = settings.decay
         self.chunks = int(os.environ.get("EXPERT_CACHE_CHUNKS", str(DEFAULT_CHUNKS)))
         self.lanes = int(os.environ.get("EXPERT_CACHE_LANES", str(DEFAULT_LANES)))
+        self.pf_chunks = int(os.environ.get("EXPERT_CACHE_PREFETCH_CHUNKS",
+                                            str(PREFETCH_CHUNKS)))
 
     def fits(self, topk_ids: torch.Tensor) -> bool:
         """Can this step be served from slots? tokens x top_k bounds the distinct experts
@@ -329,7 +338,7 @@ class ExpertSlotCache:
         if live:
             fn, name = h.expert_cache_gather_live, "expert_cache_gather_live"
             tail = (miss.data_ptr(), n_miss.data_ptr(), self.slot_expert.data_ptr(),
-                    self.chunks, self.lanes, stream)
+                    self.pf_chunks, 1, stream)
         else:
             fn, name = h.expert_cache_gather, "expert_cache_gather"
             tail = (miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, stream)

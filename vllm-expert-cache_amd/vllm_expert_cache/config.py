@@ -10,7 +10,8 @@ deployment configured for it behaves the same here:
   EXPERT_CACHE_DECAY     LFU halving period in steps, default 64, 0 = never
 
 EXPERT_CACHE_CHUNKS / EXPERT_CACHE_LANES (gather grid) are read by cache.py and
-EXPERT_CACHE_LIB (library path) by _lib.py, as in the reference.
+EXPERT_CACHE_LIB (library path) by _lib.py, as in the reference. EXPERT_CACHE_PREFETCH_CHUNKS
+(workgroups of a prefetch copy, default 16) is this package's own, read by cache.py.
 """
 from __future__ import annotations
 
