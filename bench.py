@@ -208,6 +208,7 @@ class Layers:
         self.routed = torch.zeros((L, E), dtype=torch.uint8, device=dev)
         self.step = torch.zeros((L, 1), dtype=i64, device=dev)
         self.miss = torch.zeros((L, 2 * S), dtype=i32, device=dev)
+        self.n_miss = torch.zeros((L,), dtype=i32, device=dev)
         self.fields = ("table", "map_cold", "slot_expert", "slot_stamp", "routed", "step",
                        "miss")
 
@@ -321,7 +322,7 @@ def main():
     st = Layers(torch, L, E, S, dev)
     ids_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
     out_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
-    nm_static = torch.zeros((L,), dtype=torch.int32, device=dev)
+    nm_static = st.n_miss
     nm_hist = torch.zeros((TP, L), dtype=torch.int32, device=dev)
     miss_hist = torch.zeros((TP, L, 2 * S), dtype=torch.int32, device=dev)
 
@@ -471,14 +472,14 @@ def main():
                     e0, e1, e2 = ev[i][l]
                     e0.record(stream)
                     rc = lib.expert_cache_manage_remap(
-                        *manage_args(l, row(ids_dev[t], l), row(seg_nm[i], l),
+                        *manage_args(l, row(ids_dev[t], l), row(nm_static, l),
                                      row(seg_out[i], l)), s_ptr)
                     e1.record(stream)
-                    rc |= lib.expert_cache_gather(*G_ARGS[l][:18], st.row("miss", l),
-                                                  row(seg_nm[i], l), chunks, lanes, s_ptr)
+                    rc |= lib.expert_cache_gather(*G_ARGS[l], s_ptr)
                     e2.record(stream)
                     if rc:
                         raise RuntimeError(f"launch failed rc={rc}")
+                seg_nm[i].copy_(nm_static)  # outside the event brackets
             torch.cuda.synchronize()
             man.append([[ev[i][l][0].elapsed_time(ev[i][l][1]) * 1e3 for l in range(L)]
                         for i in range(n)])
@@ -1003,7 +1004,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     ids_static = torch.zeros((L, mk), dtype=i32, device=dev)
     pred_static = torch.zeros((L, mk), dtype=i32, device=dev)
     out_static = torch.zeros((L, mk), dtype=i32, device=dev)
-    nm_static = torch.zeros((L,), dtype=i32, device=dev)
+    nm_static = st.n_miss
     nm_hist = torch.zeros((K, L), dtype=i32, device=dev)
     pf_hist = torch.zeros((K, L), dtype=i32, device=dev)
     pf_miss_hist = torch.zeros((K, L, 2 * S), dtype=i32, device=dev)
