@@ -50,9 +50,11 @@ int expert_cache_manage(const int* topk_ids, int mk, int E, int S, int max_disti
  * only for j < *n_miss, so a list with no capacity is accepted while *n_miss is 0.
  * The grid is chunks x lanes workgroups of 256 lanes; the work (miss, buffer, tile) is
  * spread over the whole grid whatever n_miss is.
- * Fails with -1 unless every b_b > 0 and b_b % 16 == 0, chunks > 0 and lanes > 0.
+ * Fails with -1 unless every b_b > 0 and b_b % 16 == 0, chunks > 0 and lanes > 0, and
+ * when n_miss is null (every launch reads *n_miss on the device).
  *
- * Replaces: kernels/expert_cache.hip:626-643 (same signature and checks);
+ * Replaces: kernels/expert_cache.hip:626-643 (same signature and checks, plus the null
+ * n_miss, which the reference's kernel would dereference);
  * bound by vllm_expert_cache/_lib.py:49-53.
  */
 int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, long b1,

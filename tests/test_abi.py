@@ -115,6 +115,13 @@ def test_gather_live_rejects_a_null_slot_table(lib):
     assert lib.expert_cache_gather_live(*args, P(1), P(1), None, 32, 1, None) == -1
 
 
+def test_gathers_reject_a_null_miss_count(lib):
+    # every launch reads *n_miss on the device; a null count is refused before any HIP call
+    args = [P(1), P(1), ctypes.c_long(16)] * 6
+    assert lib.expert_cache_gather(*args, P(1), None, 32, 1, None) == -1
+    assert lib.expert_cache_gather_live(*args, P(1), None, P(1), 32, 1, None) == -1
+
+
 def _fused(h, E, S, mi, bs, L, NB, mk=1):
     fn = h.expert_cache_fused
     fn.restype = ctypes.c_int

@@ -120,6 +120,26 @@ def test_gather_no_miss_writes_nothing():
     assert all(bool((d == 0xAB).all()) for d in store.dst)
 
 
+def test_gather_with_an_empty_miss_list_is_a_no_op():
+    # a caller with max_inserts = 0 may pass a miss list with no capacity (a null pointer
+    # here): the list is read only below n_miss, as kernels/expert_cache.hip:294-298 reads it
+    store = Expertstore(16, 8, [4096] * 6, seed=6)
+    for d in store.dst:
+        d.fill_(0x5C)
+    n_miss = torch.zeros(1, dtype=torch.int32, device=gu.DEV)
+    miss = torch.empty(0, dtype=torch.int32, device=gu.DEV)
+    slot_expert = torch.full((8,), -1, dtype=torch.int32, device=gu.DEV)
+    h = gu.lib()
+    rc = h.expert_cache_gather(*store.gather_args(), gu.ptr(miss), gu.ptr(n_miss), 32, 1,
+                               gu.stream())
+    assert rc == 0
+    rc = h.expert_cache_gather_live(*store.gather_args(), gu.ptr(miss), gu.ptr(n_miss),
+                                    gu.ptr(slot_expert), 16, 1, gu.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert all(bool((d == 0x5C).all()) for d in store.dst)
+
+
 @pytest.mark.parametrize("name", ["48-layer-e128", "8-layer-e8-bf16"])
 def test_gather_real_expert_layouts(name):
     """The workload's own expert layout and routing, one layer, default grid."""

@@ -336,7 +336,7 @@ int expert_cache_gather(void* d0, const void* s0, long b0, void* d1, const void*
   const void* const src[kGatherBufs] = {s0, s1, s2, s3, s4, s5};
   const long bytes[kGatherBufs] = {b0, b1, b2, b3, b4, b5};
   GatherArgs g;
-  if (!gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
+  if (n_miss == nullptr || !gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
   hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false, false>), dim3(chunks, lanes),
                      dim3(kGatherThreads), 0, stream, g, miss, n_miss, nullptr);
   return (int)hipGetLastError();
@@ -352,7 +352,8 @@ int expert_cache_gather_live(void* d0, const void* s0, long b0, void* d1, const 
   const void* const src[kGatherBufs] = {s0, s1, s2, s3, s4, s5};
   const long bytes[kGatherBufs] = {b0, b1, b2, b3, b4, b5};
   GatherArgs g;
-  if (slot_expert == nullptr || !gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
+  if (n_miss == nullptr || slot_expert == nullptr) return -1;
+  if (!gather_plan(dst, src, bytes, chunks, lanes, g)) return -1;
   hipLaunchKernelGGL((gather_k<kGatherUnroll, true, false, true>), dim3(chunks, lanes),
                      dim3(kGatherThreads), 0, stream, g, miss, n_miss, slot_expert);
   return (int)hipGetLastError();
