@@ -36,13 +36,16 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
                core over the trace pass, and a CPU-driven cache (that policy deciding the
                misses, one hipMemcpyAsync per (miss, buffer)) on a sample of the timed steps
   prefetch     1,024 steps of the steady-state window with and without next-layer prefetch
-               (each layer's predicted experts installed by the prefetch step and copied on
-               a side stream during an earlier layer), with no model compute and with a
-               50 us-per-layer compute stand-in; predictors of accuracy 1.0 (the true
-               routing: an upper bound) and 0.8 (each id wrong with probability 0.2), one,
-               two and four layers ahead, the prefetch step launched on its own
-               (expert_cache_prefetch) or inside the policy launch
-               (expert_cache_manage_remap_prefetch), and an insert budget of one
+               (each layer's predicted experts installed as pending by the prefetch step
+               and copied on a side stream by the live gather during an earlier layer; the
+               layer's real step keeps the routed ones and drops the rest), with no model
+               compute and with a 50 us-per-layer compute stand-in; predictors of accuracy
+               1.0 (the true routing: an upper bound) and 0.8 (each id wrong with
+               probability 0.2, the wrong guess a uniformly random expert or one the layer
+               routes elsewhere in the trace), one and two layers ahead, the prefetch step
+               launched on its own (expert_cache_prefetch) or inside the policy launch
+               (expert_cache_manage_remap_prefetch), the copy forked after the policy launch
+               or after the layer's gather, and an insert budget of one
   fused        expert_cache_fused (the LRU step plus both moe_align_block_size outputs,
                block size 16) per layer-step in graph replay, 8 layers x 256 steps of three
                workloads from a cold start; cpu_baseline.fused_us_per_layer_step times the
