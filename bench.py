@@ -591,7 +591,7 @@ def main():
     if not args.no_hit_sweep:
         sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
     manage_us = round(tw["manage_us"], 3)
-    manage_def = "HIP events around each launch (adds ~2 us per launch): an upper bound"
+    manage_def = "HIP events around each launch (adds the launch's dispatch): an upper bound"
     for x in sweep or []:
         if x.get("slots") == S and x.get("policy") == args.policy:
             manage_us = x["graph_us_per_layer"]
