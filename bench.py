@@ -115,6 +115,9 @@ def parse():
                    help="compute stand-in per layer of the prefetch leg, us, comma-separated")
     p.add_argument("--prefetch-steps", type=int, default=1024,
                    help="steps per run of the prefetch leg (at most)")
+    p.add_argument("--prefetch-from", type=int, default=None,
+                   help="trace step the prefetch leg starts from (default: the steady-state "
+                        "window's start; the warm-up step W gives the cold-start window)")
     p.add_argument("--prefetch-chunks", type=int, default=None,
                    help="workgroups of the prefetch leg's side copies (default: the "
                         "cache's prefetch grid)")
@@ -393,6 +396,8 @@ def main():
     late_starts = _spread(late0, TP, args.timing_segments, late_len) if TP - late0 >= 16 \
         else []
     pf0 = late0 if late_starts else W  # the prefetch leg starts from a steady state too
+    if args.prefetch_from is not None:
+        pf0 = min(max(args.prefetch_from, 0), TP - 1)
     snaps = {t: st.snapshot() for t in set(seg_starts) | set(late_starts) | {W, pf0}}
     run_steps(0, W, snaps)
     torch.cuda.synchronize()
