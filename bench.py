@@ -891,6 +891,11 @@ def fused_leg(torch, np, lib, dev):
             nm_hist[t].copy_(nm, non_blocking=True)
         st.restore(snap)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        # hold the stream while the steps are queued: a step is a few tens of us of GPU
+        # work, less than the host takes to queue it, so without the hold the figure would
+        # be the host's launch rate
+        torch.cuda._sleep(int(5e7))
         a.record()
         for t in range(FUSED_STEPS):
             ids_static.copy_(ids_dev[t], non_blocking=True)
@@ -911,7 +916,8 @@ def fused_leg(torch, np, lib, dev):
             f"graph replay, {int(policy_bytes + out_bytes)} algorithmic bytes per call")
     return {"bound": "latency (one wave, dependent LDS phases)", "layers": FUSED_LAYERS,
             "steps": FUSED_STEPS, "def": "graph replay of one launch per layer, including "
-            "the per-step id copy; LRU, cold start. cpu_baseline.fused_us_per_layer_step is "
+            "the per-step id copy, all steps queued behind a stream hold so the host's launch "
+            "rate is out of the figure; LRU, cold start. cpu_baseline.fused_us_per_layer_step is "
             "the oracle's fused step in C on one core with the state in host memory: it "
             "leaves out moving each step's ids to the host and the outputs back, which a "
             "CPU path would pay every layer-step", "runs": runs}

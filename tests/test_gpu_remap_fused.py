@@ -127,12 +127,14 @@ def test_fused_wide_step_is_token_ordered(mk):
 
 
 @pytest.mark.parametrize("bs", [1, 3, 16])
-def test_fused_outputs_at_any_alignment(bs):
+@pytest.mark.parametrize("name,S", [("8-layer-e256-fp8", 128), ("48-layer-e128", 16)])
+def test_fused_outputs_at_any_alignment(name, S, bs):
     """Output buffers 4 bytes past a 16-byte boundary take the scalar fill path; the bytes
-    must be the same as with aligned buffers, and nothing outside the buffers changes."""
-    w = traces.WORKLOADS["8-layer-e256-fp8"]
+    must be the same as with aligned buffers, and nothing outside the buffers changes, at
+    128 and at 8 ids per step."""
+    w = traces.WORKLOADS[name]
     ids = traces.routing(w, 1, 12)
-    E, S, mk = w.experts, 128, ids.shape[1]
+    E, mk = w.experts, ids.shape[1]
     L, NB = align_lengths(mk, E, bs)
     ref = oracle.State(E, S)
     st = gu.Layers(1, E, S)
@@ -149,3 +151,49 @@ def test_fused_outputs_at_any_alignment(bs):
         for k, v in want.items():
             assert np.array_equal(outs[k].cpu().numpy(), v), (t, k)
             assert backing[k][0].item() == -7 and backing[k][-1].item() == -7, (t, k)
+
+
+@pytest.mark.parametrize("mk", [0, 1, 7, 63, 64, 65, 200])
+@pytest.mark.parametrize("bs", [1, 5, 16, 128])
+def test_fused_random_ids_with_repeats(mk, bs):
+    """Random ids with padding and repeats (several ids per bucket, buckets of several
+    blocks), across one and several 64-id blocks of placement and block sizes that do and do
+    not divide the counts, against the oracle on every output and the state, over four
+    steps from a cold start."""
+    E, S = 96, 24
+    rng = np.random.default_rng(mk * 7 + bs)
+    L, NB = align_lengths(max(mk, 1), E, bs)
+    st, ref = gu.Layers(1, E, S), oracle.State(E, S)
+    for t in range(4):
+        ids = rng.integers(-3, E, size=mk).astype(np.int32)
+        ids[rng.random(mk) < 0.3] = rng.integers(0, 6)        # a few popular experts
+        outs = _outs(L, NB)
+        d_ids = torch.as_tensor(ids, device=gu.DEV)
+        assert _fused_call(gu.lib(), st, d_ids, mk, bs, L, NB, outs) == 0
+        rc, want = ref.fused(ids, min(E, mk), S, bs, L, NB)
+        assert rc == 0
+        torch.cuda.synchronize()
+        for k, v in want.items():
+            assert np.array_equal(outs[k].cpu().numpy(), v), (t, k)
+        assert np.array_equal(st.table[0].cpu().numpy(), ref.table), t
+        assert np.array_equal(st.slot_stamp[0].cpu().numpy(), ref.slot_stamp), t
+
+
+@pytest.mark.parametrize("mk", [8, 40, 130])
+def test_fused_outputs_clipped_to_short_buffers(mk):
+    """Buffers shorter than the padded totals (L and NB below the usual lengths): ids and
+    block ids past the end are dropped, as the reference drops them."""
+    E, S, bs = 64, 32, 4
+    rng = np.random.default_rng(mk)
+    L0, NB0 = align_lengths(mk, E, bs)
+    st, ref = gu.Layers(1, E, S), oracle.State(E, S)
+    for t, (L, NB) in enumerate(((L0 // 3, NB0 // 3), (5, 1), (L0, 2))):
+        ids = rng.integers(0, E, size=mk).astype(np.int32)
+        outs = _outs(L, NB)
+        assert _fused_call(gu.lib(), st, torch.as_tensor(ids, device=gu.DEV), mk, bs, L, NB,
+                           outs) == 0
+        rc, want = ref.fused(ids, min(E, mk), S, bs, L, NB)
+        assert rc == 0
+        torch.cuda.synchronize()
+        for k, v in want.items():
+            assert np.array_equal(outs[k].cpu().numpy(), v), (t, k)

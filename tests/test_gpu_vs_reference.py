@@ -84,9 +84,13 @@ def _graph_us(launch, reps: int) -> float:
 
 def _timed_loop(g, ids_static, ids_dev, T: int) -> float:
     """ms for T decode steps: each step copies its routing ids into the graph's input and
-    replays the graph (the graph's state is reset by the caller beforehand)."""
+    replays the graph (the graph's state is reset by the caller beforehand). Every step is
+    queued behind a stream hold before the first event."""
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    # hold the stream while the steps are queued, so that a loop whose steps are shorter
+    # than the host's launch time is not timed at the host's launch rate
+    torch.cuda._sleep(int(5e7))
     a.record()
     for t in range(T):
         ids_static.copy_(ids_dev[t], non_blocking=True)
