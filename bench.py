@@ -32,7 +32,7 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
   hit_rate     1 - inserts / distinct routed experts over the timed steps
   hit_rate_sweep  every slot budget x LFU/LRU over the whole trace from a cold start, with
                the per-layer range
-  cpu_baseline the CPU path on this box's host: the policy restated in C (oracle/) on one
+  cpu_baseline the CPU path on this machine's host: the policy restated in C (oracle/) on one
                core over the trace pass, and a CPU-driven cache (that policy deciding the
                misses, one hipMemcpyAsync per (miss, buffer)) on a sample of the timed steps
   prefetch     1,024 steps of the steady-state window with and without next-layer prefetch

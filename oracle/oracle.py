@@ -1,7 +1,8 @@
 """ctypes binding of the CPU oracle (oracle/policy.c) for numpy arrays.
 
 TEST INFRASTRUCTURE ONLY. tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
-use it as the checker / CPU baseline; the product package never imports it.
+compare results against it, or time it as the CPU baseline; the product package never
+imports it.
 
 State layout and cold/warm starts follow the reference:
   cold start  vllm_expert_cache/cache.py:84-92   (table=-1, map_cold=arange, slot_expert=-1)

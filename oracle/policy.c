@@ -2,8 +2,8 @@
  * CPU oracle for the per-layer expert-cache path (manage, remap, gather, fused align).
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product library links or calls this file. It is
- * used by tests/ as the checker, by __graft_entry__.smoke() as the checker, and by bench.py's
- * cpu_baseline leg as the CPU policy that is timed beside the GPU path.
+ * used by tests/ and __graft_entry__.smoke() to check the GPU path's results against, and
+ * by bench.py's cpu_baseline leg as the CPU policy that is timed beside the GPU path.
  *
  * It restates, in plain C, the algorithm of the reference's policy model and kernel:
  *

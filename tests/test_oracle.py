@@ -1,4 +1,4 @@
-"""Pins for the CPU oracle (oracle/policy.c), before it is trusted as the checker.
+"""Pins for the CPU oracle (oracle/policy.c), before the GPU results are checked against it.
 
   * Known answers: the reference's 12 published insert counts (README.md:177-184) on its
     own harness's traces (tests/compare_policies.py:31-93), regenerated with numpy.
