@@ -45,6 +45,55 @@ def test_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), name
 
 
+_C_CALLER = r"""
+#include <stdio.h>
+#include "expert_cache.h"
+
+int main(void) {
+  int bad = 0;
+  /* E = 0, S = 0, a null n_miss, chunks = 0, L = 0: each is refused before any HIP call */
+  bad += expert_cache_manage(0, 1, 0, 4, 1, 4, 0, 0, 0, 0, 0, 0, 0, 0, 1, 64, 0) != -1;
+  bad += expert_cache_manage_remap(0, 4, 1, 8, 0, 1, 4, 0, 0, 0, 0, 0, 0, 0, 0, 1, 64, 0, 0)
+         != -1;
+  bad += expert_cache_gather((void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                             (void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                             (void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                             (const int*)1, 0, 32, 1, 0) != -1;
+  bad += expert_cache_gather_live((void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                                  (void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                                  (void*)1, (const void*)1, 16, (void*)1, (const void*)1, 16,
+                                  (const int*)1, (const int*)1, (const int*)1, 0, 1, 0) != -1;
+  bad += expert_cache_fused(0, 1, 8, 4, 1, 4, 0, 0, 0, 0, 0, 0, 0, 0, 16, 0, 1, 0, 0, 0, 0, 0,
+                            0, 0) != -1;
+  bad += expert_cache_remap(0, 1, 3, 0, 8, 0, 0) != -1;
+  bad += expert_cache_prefetch(0, 1, 0, 4, 4, 0, 0, 0, 0, 0, 0, 0, 0) != -1;
+  printf("%d\n", bad);
+  return bad;
+}
+"""
+
+
+def test_header_compiles_as_c_and_links(tmp_path):
+    """A plain C11 caller (gcc, no HIP headers) compiles against include/expert_cache.h with
+    every warning an error, links against the library, and gets -1 from each refused call."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    src = tmp_path / "caller.c"
+    src.write_text(_C_CALLER)
+    so = Path(_lib.library_path())
+    exe = tmp_path / "caller"
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", f"-I{HEADER.parent}",
+                    str(src), "-o", str(exe), f"-L{so.parent}", f"-l:{so.name}",
+                    f"-Wl,-rpath,{so.parent}"], check=True, capture_output=True, text=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert res.stdout.strip() == "0"
+
+
 def test_library_path_order(tmp_path, monkeypatch):
     fake = tmp_path / "libexpertcache.so"
     fake.write_bytes(b"")
