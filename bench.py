@@ -123,6 +123,9 @@ def parse():
                         "cache's prefetch grid)")
     p.add_argument("--no-fused", action="store_true",
                    help="skip the expert_cache_fused leg")
+    p.add_argument("--no-chain", action="store_true",
+                   help="skip the decode chain's per-node costs (graph substitution over the "
+                        "trace pass)")
     p.add_argument("--routes", default=None,
                    help="replay a recorded trace instead of the synthetic routing: an npz "
                         "whose ids are [T, L, mk] with -1 padding (the reference's routes.npz "
@@ -517,65 +520,44 @@ def main():
     st.restore(final)
 
     # ---- host->device link peak -------------------------------------------------------------
-    n_peak = 256 << 20
-    src = torch.empty(n_peak, dtype=torch.uint8, pin_memory=True)
-    dst = torch.empty(n_peak, dtype=torch.uint8, device=dev)
-    for _ in range(2):
-        dst.copy_(src, non_blocking=True)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(5):
-        dst.copy_(src, non_blocking=True)
-    b.record()
-    torch.cuda.synchronize()
-    memcpy_gbps = 5 * n_peak / (a.elapsed_time(b) * 1e-3) / 1e9
-    one = torch.tensor([0, 0], dtype=torch.int32, device=dev)
-    one_n = torch.tensor([1], dtype=torch.int32, device=dev)
-    big = [ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(device_address(src)),
-           ctypes.c_long(n_peak)] * 6
-    tail = (ctypes.c_void_p(one.data_ptr()), ctypes.c_void_p(one_n.data_ptr()), chunks, lanes,
-            s_ptr)
-    for _ in range(2):
-        assert lib.expert_cache_gather(*big, *tail) == 0
-    torch.cuda.synchronize()
-    a.record()
-    for _ in range(5):
-        lib.expert_cache_gather(*big, *tail)
-    b.record()
-    torch.cuda.synchronize()
-    kernel_gbps = 5 * n_peak / (a.elapsed_time(b) * 1e-3) / 1e9
-    peak = max(memcpy_gbps, kernel_gbps)
-    log(f"link peak: hipMemcpyAsync H2D {memcpy_gbps:.2f} GB/s, gather kernel on one 256 MB "
-        f"slab {kernel_gbps:.2f} GB/s")
-    del src, dst
+    peak, peak_detail = link_peak(torch, lib, s_ptr, dev)
 
-    # ---- latency floor: an empty kernel node in a graph (48 per replay) --------------------
+    # ---- latency floor: an empty kernel node in a graph of L, replays behind a hold --------
+    hold = Hold(torch)
     ge = torch.cuda.CUDAGraph()
     with torch.cuda.graph(ge):
         for _ in range(L):
             torch.cuda._sleep(0)
     ge.replay()
     torch.cuda.synchronize()
-    a.record()
-    for _ in range(200):
-        ge.replay()
-    b.record()
-    torch.cuda.synchronize()
-    empty_us = a.elapsed_time(b) * 1e3 / (200 * L)
+    empty_s = sum(s for _, _, s in hold.time(0, 256, lambda t: ge.replay()))
+    empty_us = empty_s * 1e6 / (256 * L)
     del ge
-    log(f"empty kernel node in a graph: {empty_us:.2f} us")
+    log(f"empty kernel node in a graph of {L}: {empty_us:.2f} us")
+
+    # ---- the decode chain's per-node costs, by substitution --------------------------------
+    chain = None if args.no_chain else chain_costs(
+        torch, lib, hold, graph, M_ARGS, gather_args, st, snaps[W], final, ids_dev,
+        ids_static, nm_hist, miss_hist, nm[:TP], W, TP, late0, L, S, B_exp, chunks, lanes,
+        peak, dev)
+    verified["chain_rerun_state"] = None if chain is None else chain.pop("rerun_state_equal")
+    stamps = None if args.no_chain else chain_stamps(
+        torch, np, hold, M_ARGS, G_ARGS, st, snaps[W], final, ids_dev, ids_static, nm[:TP], W,
+        TP, late0, L, B_exp, chunks * lanes, peak, dev)
+    verified["stamped_rerun_state"] = None if stamps is None else \
+        stamps.pop("rerun_state_equal")
+    if chain is not None:
+        chain["stamps"] = stamps
 
     # ---- CPU baseline: C policy on one core + hipMemcpyAsync per (miss, buffer); the same --
     # ---- C policy over the trace pass checks the GPU's states ----------------------------
+    check, policy_timing = oracle_check(np, ids_np, L, E, S, policy, decay, TP, nm[:TP],
+                                        miss_hist.cpu().numpy(), final)
+    verified.update(check)
     cpu = None
     if args.cpu_steps > 0:
-        cpu, check = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E,
-                                  S, mk, policy, decay, W, TP, nm[:TP],
-                                  miss_hist.cpu().numpy(), final)
-        verified.update(check)
-    verified["all"] = all(verified[k] is not False for k in
-                          ("slot_bytes", "state", "n_miss_per_step", "miss_lists_per_step"))
+        cpu = cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snaps[W], L, E, S, mk,
+                           policy, decay, W, policy_timing)
 
     prefetch = None
     if not args.no_prefetch:
@@ -585,24 +567,29 @@ def main():
         pw = max(32, min(args.prefetch_steps, int(130e9 / per_step)))
         prefetch = prefetch_leg(torch, np, lib, ids_np, ids_dev, G_ARGS, snaps[pf0], L, E, S,
                                 mk, policy, decay, pf0, min(steps, pf0 + pw), B_exp, chunks,
-                                lanes, dev, peak, window=pw,
+                                lanes, dev, peak, slots, content, bufs, window=pw,
                                 pf_chunks=args.prefetch_chunks or PREFETCH_CHUNKS,
                                 compute=tuple(float(c) for c in
                                               args.prefetch_compute.split(",")))
+    verified["prefetch"] = None if prefetch is None else prefetch["verified"]["all"]
 
-    fused = None if args.no_fused else fused_leg(torch, np, lib, dev)
+    fused = None if args.no_fused else fused_leg(torch, np, lib, dev, hold)
 
     sweep = None
     if not args.no_hit_sweep:
-        sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev)
-    manage_us = round(tw["manage_us"], 3)
-    manage_def = "HIP events around each launch (adds the launch's dispatch): an upper bound"
-    for x in sweep or []:
-        if x.get("slots") == S and x.get("policy") == args.policy:
-            manage_us = x["graph_us_per_layer"]
-            manage_def = (f"in-graph cost per layer of the policy+remap kernel alone over the "
-                          f"whole {x['steps']}-step trace at this budget and policy "
-                          f"(hit-rate pass)")
+        sweep = hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev, hold)
+    if chain is not None:
+        manage_us = chain["trace_pass"]["manage_remap_us_per_layer"]
+        manage_def = chain["manage_remap_def"]
+    else:
+        manage_us = round(tw["manage_us"], 3)
+        manage_def = "HIP events around each launch (adds the launch's dispatch): an upper bound"
+    policy_graph_us = next((x["graph_us_per_layer"] for x in sweep or []
+                            if x.get("slots") == S and x.get("policy") == args.policy), None)
+    verified["all"] = all(verified[k] is True for k in
+                          ("slot_bytes", "state", "n_miss_per_step", "miss_lists_per_step")) \
+        and all(verified[k] is not False for k in ("chain_rerun_state", "stamped_rerun_state",
+                                                   "prefetch"))
 
     traffic = _traffic()
 
@@ -637,18 +624,38 @@ def main():
         "trace_pass": trace_pass,
         "manage_remap_us_per_layer": manage_us,
         "manage_remap_def": manage_def,
+        "manage_remap_us_per_layer_steady_state":
+            None if chain is None else chain["steady_state"]["manage_remap_us_per_layer"],
+        "manage_remap_over_empty_node_us":
+            None if chain is None else chain["trace_pass"]["manage_remap_over_empty_node_us"],
+        "empty_node_in_chain_us":
+            None if chain is None else chain["trace_pass"]["empty_node_us"],
+        "manage_remap_kernel_us_in_chain":
+            None if stamps is None else stamps["chain"]["trace_pass"]["policy_us"]["mean"],
+        "manage_remap_us_per_layer_policy_graph": policy_graph_us,
         "manage_remap_us_per_layer_events": round(tw["manage_us"], 3),
         "empty_kernel_graph_us": round(empty_us, 3),
+        "decode_chain": chain,
         "manage_remap_counters": _manage_counters(),
         "gather_us_per_launch": round(tw["gather_us"], 3),
         "gather_GBps_launches_with_miss": rounded(tw["with_miss"]),
         "gather_us_launch_without_miss": rounded(tw["zero_us"]),
-        "link_peak_GBps": {"hipMemcpyAsync_h2d": round(memcpy_gbps, 3),
-                           "gather_kernel_256MB": round(kernel_gbps, 3)},
+        "link_peak": peak_detail,
         "roofline": {"bound": "host-link", "kernel": "gather_k",
                      "achieved": round(tw["achieved"], 3),
                      "peak": round(peak, 3), "unit": "GB/s",
                      "frac": round(tw["achieved"] / peak, 4),
+                     "frac_trace_pass": None if chain is None
+                     else chain["trace_pass"]["gather_frac"],
+                     "frac_steady_state": None if chain is None
+                     else chain["steady_state"]["gather_frac"],
+                     "frac_trace_pass_kernel": None if stamps is None
+                     else stamps["chain"]["trace_pass"]["gather_kernel_frac"],
+                     "frac_steady_state_kernel": None if stamps is None
+                     else stamps["chain"]["steady_state"]["gather_kernel_frac"],
+                     "frac_trace_pass_whole_job": round(trace_pass["GBps"] / peak, 4),
+                     "inserts_per_launch_steady": round(float(nm[late0:TP].sum()) /
+                                                        max(1, (TP - late0) * L), 4),
                      "achieved_launches_with_miss": rounded(tw["with_miss"]),
                      "frac_launches_with_miss": None if tw["with_miss"] is None
                      else round(tw["with_miss"] / peak, 4),
@@ -663,9 +670,20 @@ def main():
                                      f"achieved_launches_with_miss counts only launches that "
                                      f"copy, gather_us_launch_without_miss is the rest's cost; "
                                      f"steady_state is the same over the second half of the "
-                                     f"trace pass",
-                     "peak_def": "measured: max(hipMemcpyAsync H2D 256 MB pinned, gather "
-                                 "kernel on one 256 MB slab)",
+                                     f"trace pass. frac_trace_pass and frac_steady_state: "
+                                     f"gathered bytes / what the gather nodes add to the "
+                                     f"decode graph (its time minus the time of the same "
+                                     f"graph without them) over trace steps {W}..{TP} and "
+                                     f"{late0}..{TP}, no events or profiler in the chain "
+                                     f"(decode_chain); frac_trace_pass_kernel and "
+                                     f"frac_steady_state_kernel: gathered bytes / the gather "
+                                     f"kernels' own durations in the same windows, from clock "
+                                     f"stamps inside stamped copies of the kernels "
+                                     f"(decode_chain.stamps); frac_trace_pass_whole_job: "
+                                     f"trace_pass.GBps, the whole step's wall time",
+                     "peak_def": "measured: the best single repetition of hipMemcpyAsync H2D "
+                                 "of 2 GiB pinned and of the gather kernel on one 2 GiB slab "
+                                 "(16, 32 and 64 workgroups), 3 repetitions each (link_peak)",
                      "steady_state": None if late is None else {
                          "trace_steps": [late0, TP], "trace_inserts": int(nm[late0:TP].sum()),
                          "segments": len(late_starts),
@@ -688,6 +706,335 @@ def main():
         sys.exit(1)
 
 
+class Hold:
+    """Times short GPU work with stream holds: each chunk of steps is queued behind a spin
+    kernel on the current stream, so the GPU runs the chunk back to back instead of at the
+    rate the host queues it. The hold is sized from the host's queueing time of the previous
+    chunk; a chunk that took the host longer to queue than its hold is counted in `late`
+    (the GPU may have waited for the host there)."""
+
+    def __init__(self, torch, first_us=20000.0, min_us=1000.0):
+        self.torch = torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(int(2e6))
+        b.record()
+        torch.cuda.synchronize()
+        self.cyc_per_us = 2e6 / (a.elapsed_time(b) * 1e3)
+        self.hold_us, self.first_us, self.min_us = first_us, first_us, min_us
+        self.chunks = self.late = 0
+
+    def time(self, lo, hi, enqueue, chunk=16, cuts=()):
+        """Runs enqueue(t) for t in [lo, hi) in chunks that end at multiples of `chunk` and
+        at each of `cuts`; returns [(c0, c1, GPU seconds of chunk [c0, c1))]."""
+        torch = self.torch
+        pts = sorted({lo, hi} | {c for c in cuts if lo < c < hi} |
+                     set(range((lo // chunk + 1) * chunk, hi, chunk)))
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        out = []
+        self.hold_us = self.first_us
+        for c0, c1 in zip(pts[:-1], pts[1:]):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(self.hold_us * self.cyc_per_us))
+            a.record()
+            h0 = time.perf_counter()
+            for t in range(c0, c1):
+                enqueue(t)
+            host_us = (time.perf_counter() - h0) * 1e6
+            b.record()
+            torch.cuda.synchronize()
+            out.append((c0, c1, a.elapsed_time(b) * 1e-3))
+            self.chunks += 1
+            self.late += host_us > self.hold_us
+            self.hold_us = max(self.min_us, 2.0 * host_us)
+        return out
+
+    def record(self):
+        return {"chunks": self.chunks, "late_chunks": self.late,
+                "spin_cycles_per_us": round(self.cyc_per_us, 1)}
+
+
+def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, ids_dev,
+                ids_static, nm_hist, miss_hist, nm, W, TP, late0, L, S, B_exp, chunks, lanes,
+                peak, dev):
+    """What each node of the decode graph costs inside the chain, measured by substitution:
+    the graph's step time against the same step with some of its nodes taken out or
+    replaced, each replayed over the same trace steps behind stream holds. No events sit
+    between the nodes and no profiler is attached, so every figure is the chain's own.
+
+      full         the decode graph: per layer the policy+remap launch, then the gather
+      gathers      per layer only the gather, of the miss list the full graph recorded at
+                   that step and layer (copied in per step, so the same bytes move)
+      empty+gather per layer an empty kernel node in place of the policy launch, then the
+                   same gather
+      policy       per layer only the policy+remap launch
+
+    Every variant copies the step's routing ids and recorded miss lists into its inputs
+    before the replay, so the per-step copies cancel in the differences:
+      policy+remap per layer = (full - gathers) / (steps x L)
+      empty node per layer   = (empty+gather - gathers) / (steps x L)
+      gather per launch      = (full - policy) / (steps x L), and the gather's in-chain rate
+                               is the gathered bytes over (full - policy).
+    The policy and full variants restart from the snapshot at step W; the full variant's
+    final state must equal the trace pass's (rerun_state_equal)."""
+    i32 = torch.int32
+    # recorded miss lists as gather inputs: row l = [n_miss, e0, s0, e1, s1, ...]
+    rec_dev = torch.cat([nm_hist[:TP, :, None], miss_hist[:TP]], dim=2).contiguous()
+    rec_static = torch.zeros((L, 1 + 2 * S), dtype=i32, device=dev)
+    rs = rec_static.stride(0) * rec_static.element_size()
+    rec_args = [tuple(gather_args(l)) + (ctypes.c_void_p(rec_static.data_ptr() + l * rs + 4),
+                                         ctypes.c_void_p(rec_static.data_ptr() + l * rs),
+                                         chunks, lanes) for l in range(L)]
+
+    def capture(launch):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            launch(s)
+        torch.cuda.synchronize()
+        return g
+
+    def gathers(s, empty=False):
+        for l in range(L):
+            if empty:
+                torch.cuda._sleep(0)
+            if lib.expert_cache_gather(*rec_args[l], s):
+                raise RuntimeError("gather launch failed")
+
+    def policy(s):
+        for l in range(L):
+            if lib.expert_cache_manage_remap(*m_args[l], s):
+                raise RuntimeError("policy launch failed")
+
+    variants = {"gathers": capture(gathers), "empty+gather": capture(
+        lambda s: gathers(s, empty=True)), "policy": capture(policy), "full": graph}
+    times = {}
+    for name, g in variants.items():
+        def enqueue(t, g=g):
+            ids_static.copy_(ids_dev[t], non_blocking=True)
+            rec_static.copy_(rec_dev[t], non_blocking=True)
+            g.replay()
+
+        if name in ("policy", "full"):
+            st.restore(snap)
+        times[name] = hold.time(W, TP, enqueue, cuts=(late0,))
+        log(f"decode chain, {name}: {sum(x[2] for x in times[name]):.4f} s over steps "
+            f"{W}..{TP}")
+    rerun_equal = all(torch.equal(getattr(st, f), final[f]) for f in st.fields)
+    for name in ("gathers", "empty+gather", "policy"):
+        del variants[name]
+
+    def window(lo):
+        n = TP - lo
+        t = {k: sum(s for c0, _, s in v if c0 >= lo) for k, v in times.items()}
+        per = 1e6 / (n * L)
+        moved = float(nm[lo:TP].sum()) * B_exp
+        gather_s = t["full"] - t["policy"]
+        return {"trace_steps": [lo, TP],
+                "ms_per_step": round(1e3 * t["full"] / n, 4),
+                "manage_remap_us_per_layer": round((t["full"] - t["gathers"]) * per, 3),
+                "empty_node_us": round((t["empty+gather"] - t["gathers"]) * per, 3),
+                "manage_remap_over_empty_node_us":
+                    round((t["full"] - t["empty+gather"]) * per, 3),
+                "policy_graph_us_per_layer": round(t["policy"] * per, 3),
+                "gather_us_per_launch": round(gather_s * per, 3),
+                "gather_GBps": round(moved / gather_s / 1e9, 3),
+                "gather_frac": round(moved / gather_s / 1e9 / peak, 4),
+                "inserts": int(nm[lo:TP].sum()),
+                "seconds": {k: round(v, 5) for k, v in t.items()}}
+
+    out = {"trace_pass": window(W), "steady_state": window(late0),
+           "hold": hold.record(), "rerun_state_equal": rerun_equal,
+           "manage_remap_def": f"what the policy+remap launch adds to the decode graph per "
+                               f"layer, over trace steps {W}..{TP}: the graph's time minus "
+                               f"that of the same graph with only its gathers (fed the "
+                               f"recorded miss lists), per layer-step; no events or "
+                               f"profiler in the chain (decode_chain)",
+           "def": chain_costs.__doc__.split("\n\n")[1].strip()}
+    tp, ss = out["trace_pass"], out["steady_state"]
+    log(f"decode chain over steps {W}..{TP}: policy+remap {tp['manage_remap_us_per_layer']} "
+        f"us/layer (empty node {tp['empty_node_us']}, policy-only graph "
+        f"{tp['policy_graph_us_per_layer']}), gather {tp['gather_GBps']} GB/s "
+        f"({tp['gather_frac']}); steady state from {late0}: policy+remap "
+        f"{ss['manage_remap_us_per_layer']} us/layer, gather {ss['gather_GBps']} GB/s "
+        f"({ss['gather_frac']}); re-run state {'equal' if rerun_equal else 'MISMATCH'}")
+    return out
+
+
+def _stamps_lib():
+    """bench_stamps.so (bench_stamps.hip, built by __graft_entry__.build()), bound."""
+    from vllm_expert_cache._lib import SIGNATURES
+
+    path = ROOT / "bench_stamps.so"
+    if not path.is_file():
+        raise FileNotFoundError(f"{path} missing: run __graft_entry__.build()")
+    h = ctypes.CDLL(str(path))
+    P = ctypes.c_void_p
+    for name, base in (("stamped_manage_remap", "expert_cache_manage_remap"),
+                       ("stamped_gather", "expert_cache_gather")):
+        f = getattr(h, name)
+        f.restype = ctypes.c_int
+        f.argtypes = SIGNATURES[base][:-1] + [P, P]  # ... row(s), stream
+    h.stamped_empty.restype = ctypes.c_int
+    h.stamped_empty.argtypes = [P, P]
+    return h
+
+
+def chain_stamps(torch, np, hold, m_args, g_args, st, snap, final, ids_dev, ids_static, nm,
+                 W, TP, late0, L, B_exp, grid, peak, dev):
+    """The decode chain's kernel times from inside the kernels: the decode graph rebuilt
+    with bench_stamps.so's stamped copies of the policy+remap and gather kernels (the
+    product's device code between two reads of the GPU's constant-rate clock) and replayed
+    over trace steps W..TP from the snapshot at W, the stamps of every launch kept. Then the
+    same with the policy launches alone (back to back). Per window (the trace pass, and the
+    steady state from late0):
+      policy_us        the policy+remap kernel, first instruction to its stores completed
+      into_policy_us   the previous layer's gather ending (its last workgroup) to the policy
+                       kernel's first instruction: what the chain takes to start it
+      into_gather_us   the policy kernel's end to the gather's first workgroup starting
+      gather_us        the gather's first workgroup starting to its last one ending, for
+                       launches without a miss and with one
+      gather_kernel_GBps  gathered bytes / summed gather durations: the kernel-only rate
+    The first layer of each step is left out of the gap figures (the per-step copies sit
+    before it). The stamped run's final state must equal the trace pass's."""
+    sl = _stamps_lib()
+    rows = torch.zeros((L, 1 + grid, 2), dtype=torch.int64, device=dev)
+    n = TP - W
+    hist = torch.zeros((n, L, 1 + grid, 2), dtype=torch.int64, device=dev)
+
+    def rp(l, k):
+        return ctypes.c_void_p(rows.data_ptr() + (l * (1 + grid) + k) * 16)
+
+    # the clock's rate: two stamped empty kernels around a spin, against HIP events
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    a.record()
+    assert sl.stamped_empty(rp(0, 0), s0) == 0
+    torch.cuda._sleep(int(50000 * hold.cyc_per_us))
+    assert sl.stamped_empty(rp(1, 0), s0) == 0
+    b.record()
+    torch.cuda.synchronize()
+    r = rows.cpu().numpy()
+    mhz = (r[1, 0, 0] - r[0, 0, 0]) / (a.elapsed_time(b) * 1e3)
+
+    def capture(policy_only):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for l in range(L):
+                rc = sl.stamped_manage_remap(*m_args[l], rp(l, 0), s)
+                if not policy_only:
+                    rc |= sl.stamped_gather(*g_args[l], rp(l, 1), s)
+                if rc:
+                    raise RuntimeError(f"stamped launch failed rc={rc}")
+        torch.cuda.synchronize()
+        return g
+
+    out = {"clock_MHz": round(float(mhz), 2)}
+    for name in ("chain", "policy_only"):
+        g = capture(name == "policy_only")
+        st.restore(snap)
+        rows.zero_()
+
+        def enqueue(t):
+            ids_static.copy_(ids_dev[t], non_blocking=True)
+            g.replay()
+            hist[t - W].copy_(rows, non_blocking=True)
+
+        hold.time(W, TP, enqueue)
+        del g
+        if name == "chain":
+            out["rerun_state_equal"] = all(torch.equal(getattr(st, f), final[f])
+                                           for f in st.fields)
+        h = hist.cpu().numpy().astype(np.float64) / mhz  # us
+        out[name] = {}
+        for wname, lo in (("trace_pass", W), ("steady_state", late0)):
+            x = h[lo - W:]
+            pol = x[:, :, 0, 1] - x[:, :, 0, 0]
+            fig = {"trace_steps": [lo, TP], "policy_us": _stats(np, pol)}
+            if name == "chain":
+                g0, g1 = x[:, :, 1:, 0].min(-1), x[:, :, 1:, 1].max(-1)
+                gat = g1 - g0
+                moved = nm[lo:TP] > 0
+                fig["into_policy_us"] = _stats(np, x[:, 1:, 0, 0] - g1[:, :-1])
+                fig["into_gather_us"] = _stats(np, g0[:, 1:] - x[:, 1:, 0, 1])
+                fig["gather_us_without_miss"] = _stats(np, gat[~moved])
+                fig["gather_us_with_miss"] = _stats(np, gat[moved])
+                nbytes = float(nm[lo:TP].sum()) * B_exp
+                fig["gather_kernel_GBps"] = round(nbytes / (gat.sum() * 1e-6) / 1e9, 3)
+                fig["gather_kernel_frac"] = round(fig["gather_kernel_GBps"] / peak, 4)
+                fig["gather_kernel_GBps_launches_with_miss"] = round(
+                    nbytes / (gat[moved].sum() * 1e-6) / 1e9, 3) if moved.any() else None
+                fig["layer_us"] = round(float((x[:, 1:, 1:, 1].max(-1) -
+                                               g1[:, :-1]).mean()), 3)
+            else:
+                fig["into_policy_us"] = _stats(np, x[:, 1:, 0, 0] - x[:, :-1, 0, 1])
+            out[name][wname] = fig
+    c, p = out["chain"]["trace_pass"], out["policy_only"]["trace_pass"]
+    log(f"stamps (clock {mhz:.1f} MHz), trace pass: policy+remap kernel "
+        f"{c['policy_us']['mean']} us in the chain (p50 {c['policy_us']['p50']}), "
+        f"{p['policy_us']['mean']} us back to back; into policy {c['into_policy_us']['mean']}, "
+        f"into gather {c['into_gather_us']['mean']} us; gather kernel-only "
+        f"{c['gather_kernel_GBps']} GB/s ({c['gather_kernel_frac']}); steady state "
+        f"{out['chain']['steady_state']['gather_kernel_GBps']} GB/s")
+    out["def"] = " ".join(chain_stamps.__doc__.split("\n\n")[0].split())
+    return out
+
+
+def _stats(np, x):
+    x = np.asarray(x, dtype=np.float64).ravel()
+    if x.size == 0:
+        return None
+    return {"mean": round(float(x.mean()), 3), "p10": round(float(np.percentile(x, 10)), 3),
+            "p50": round(float(np.median(x)), 3), "p90": round(float(np.percentile(x, 90)), 3),
+            "n": int(x.size)}
+
+
+def link_peak(torch, lib, s_ptr, dev, n_bytes=2 << 30, reps=3, grids=(16, 32, 64)):
+    """The host->device link's peak, measured: hipMemcpyAsync H2D of n_bytes from pinned
+    memory, and the gather kernel copying one n_bytes slab on grids of 16, 32 and 64
+    workgroups; each `reps` times after a warm-up, HIP events around each. The peak is the
+    best single repetition of any method."""
+    from vllm_expert_cache.cache import device_address
+
+    src = torch.empty(n_bytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(n_bytes, dtype=torch.uint8, device=dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def reps_of(launch):
+        launch()
+        torch.cuda.synchronize()
+        got = []
+        for _ in range(reps):
+            a.record()
+            launch()
+            b.record()
+            torch.cuda.synchronize()
+            got.append(n_bytes / (a.elapsed_time(b) * 1e-3) / 1e9)
+        return {"best": round(max(got), 3), "min": round(min(got), 3),
+                "reps": [round(g, 3) for g in got]}
+
+    out = {"hipMemcpyAsync_h2d": reps_of(lambda: dst.copy_(src, non_blocking=True))}
+    pair = torch.tensor([0, 0], dtype=torch.int32, device=dev)
+    one = torch.tensor([1], dtype=torch.int32, device=dev)
+    big = [ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(device_address(src)),
+           ctypes.c_long(n_bytes)] * 6
+    for g in grids:
+        def launch(g=g):
+            if lib.expert_cache_gather(*big, ctypes.c_void_p(pair.data_ptr()),
+                                       ctypes.c_void_p(one.data_ptr()), g, 1, s_ptr):
+                raise RuntimeError("gather launch failed")
+        out[f"gather_kernel_{g}x1"] = reps_of(launch)
+    del src, dst
+    peak = max(v["best"] for v in out.values())
+    spread = max(v["best"] for v in out.values()) - min(v["min"] for v in out.values())
+    log("link peak: " + ", ".join(f"{k} best {v['best']:.2f} (min {v['min']:.2f})"
+                                  for k, v in out.items()) + f" GB/s -> {peak:.2f}")
+    return peak, {"methods": out, "bytes_per_rep": n_bytes, "spread_GBps": round(spread, 3)}
+
+
 def _spread(lo, hi, n, length):
     """n segment starts of `length` steps spread evenly over [lo, hi)."""
     n = max(1, n)
@@ -696,15 +1043,11 @@ def _spread(lo, hi, n, length):
     return sorted({lo + (k * (hi - lo - length)) // (n - 1) for k in range(n)})
 
 
-def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, policy, decay,
-                 W, TP, gpu_nm, gpu_miss, gpu_final):
-    """The CPU path on this host, and the check of the GPU's trace pass.
+def oracle_check(np, ids_np, L, E, S, policy, decay, TP, gpu_nm, gpu_miss, gpu_final):
+    """The check of the GPU's trace pass against the oracle, and the oracle's policy timing.
 
     Timed: the oracle's C policy (oracle/policy.c, one core) over the trace pass from a
-    cold start, every layer; the same over 16 host threads; and the CPU-driven cache over a
-    bounded sample (the first cpu_steps timed steps from the same start state): the C policy
-    decides each layer's misses and each (miss, buffer) is one hipMemcpyAsync from pinned
-    host memory into the slot.
+    cold start, every layer; the same over up to 16 host threads.
 
     Checked: the oracle's per-step n_miss and miss lists over the trace pass, and its final
     state, against what the GPU's graph produced (gpu_nm [TP, L], gpu_miss [TP, L, 2S],
@@ -738,6 +1081,24 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         f"{'equal' if nm_ok else 'MISMATCH'}, miss lists {'equal' if miss_ok else 'MISMATCH'}, "
         f"final state {'equal' if state_ok else 'MISMATCH'}")
     check = {"state": state_ok, "n_miss_per_step": nm_ok, "miss_lists_per_step": miss_ok}
+    timing = {"policy_us_per_layer_step": round(policy_us, 4),
+              "policy_sample": f"trace steps 0..{TP} x {L} layers from a cold start",
+              "policy_us_per_layer_step_threads": round(policy_par_us, 4),
+              "policy_threads": threads}
+    log(f"oracle policy: {policy_us:.3f} us/layer-step (one core), {policy_par_us:.3f} "
+        f"us/layer-step over {threads} threads")
+    return check, timing
+
+
+def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, policy, decay,
+                 W, policy_timing):
+    """The CPU path on this host: the CPU-driven cache over a bounded sample (the first
+    cpu_steps timed steps from the timed window's start state): the oracle's C policy
+    (oracle/policy.c, one core) decides each layer's misses and each (miss, buffer) is one
+    hipMemcpyAsync from pinned host memory into the slot. policy_timing is the oracle's
+    policy timing from oracle_check."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
 
     states = []
     for l in range(L):
@@ -773,21 +1134,16 @@ def cpu_baseline(args, torch, np, ids_np, host, slots, bufs, snap, L, E, S, mk, 
         hbuf.copy_(hsrc)
     host_memcpy = 4 * (256 << 20) / (time.perf_counter() - t1) / 1e9
     log(f"cpu baseline: {n} steps x {L} layers, {moved / 1e9:.2f} GB in {wall:.2f}s -> "
-        f"{moved / wall / 1e9:.2f} GB/s; policy {policy_us:.3f} us/layer-step (one core), "
-        f"{policy_par_us:.3f} us/layer-step over {threads} threads; host memcpy "
-        f"{host_memcpy:.1f} GB/s")
+        f"{moved / wall / 1e9:.2f} GB/s; host memcpy {host_memcpy:.1f} GB/s")
     return {"value": round(moved / wall / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"trace steps {W}..{W + n} x {L} layers from the timed steps' start "
                       f"state: C policy (oracle/policy.c) per layer-step, then one "
                       f"hipMemcpyAsync H2D per (miss, buffer)",
-            "policy_us_per_layer_step": round(policy_us, 4),
-            "policy_sample": f"trace steps 0..{TP} x {L} layers from a cold start",
-            "policy_us_per_layer_step_threads": round(policy_par_us, 4),
-            "policy_threads": threads,
+            **policy_timing,
             "host_memcpy_GBps": round(host_memcpy, 2),
             "fused_us_per_layer_step": None if args.no_fused else _cpu_fused(np, oracle),
             "pcie_round_trip_us_per_layer_step": _pcie_round_trip(torch),
-            "cpu": _cpu_model(), "nproc": os.cpu_count()}, check
+            "cpu": _cpu_model(), "nproc": os.cpu_count()}
 
 
 def _pcie_round_trip(torch, n=2000):
@@ -841,7 +1197,7 @@ def _cpu_fused(np, oracle):
     return out
 
 
-def fused_leg(torch, np, lib, dev):
+def fused_leg(torch, np, lib, dev, hold):
     """expert_cache_fused per layer-step: FUSED_LAYERS launches captured in one graph,
     replayed for FUSED_STEPS steps of each FUSED_CASES workload from a cold start, the
     step's ids copied into the graph's input first. The kernel is latency-bound; its
@@ -890,20 +1246,17 @@ def fused_leg(torch, np, lib, dev):
             g.replay()
             nm_hist[t].copy_(nm, non_blocking=True)
         st.restore(snap)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        # hold the stream while the steps are queued: a step is a few tens of us of GPU
-        # work, less than the host takes to queue it, so without the hold the figure would
-        # be the host's launch rate
-        torch.cuda._sleep(int(5e7))
-        a.record()
-        for t in range(FUSED_STEPS):
+        # steps queued behind stream holds: a step is a few tens of us of GPU work, less
+        # than the host takes to queue it, so without the holds the figure would be the
+        # host's launch rate
+
+        def enqueue(t):
             ids_static.copy_(ids_dev[t], non_blocking=True)
             g.replay()
-        b.record()
-        torch.cuda.synchronize()
+
+        sec = sum(x[2] for x in hold.time(0, FUSED_STEPS, enqueue))
         del g
-        us = a.elapsed_time(b) * 1e3 / (FUSED_STEPS * Ly)
+        us = sec * 1e6 / (FUSED_STEPS * Ly)
         inserts = float(nm_hist.float().mean())
         policy_bytes = 4 * mk + 2 * (8 * E + 12 * S + 8) + 8 * inserts + 4
         out_bytes = 2 * (4 * L + 4 * NB + 4)
@@ -916,8 +1269,8 @@ def fused_leg(torch, np, lib, dev):
             f"graph replay, {int(policy_bytes + out_bytes)} algorithmic bytes per call")
     return {"bound": "latency (one wave, dependent LDS phases)", "layers": FUSED_LAYERS,
             "steps": FUSED_STEPS, "def": "graph replay of one launch per layer, including "
-            "the per-step id copy, all steps queued behind a stream hold so the host's launch "
-            "rate is out of the figure; LRU, cold start. cpu_baseline.fused_us_per_layer_step is "
+            "the per-step id copy, steps queued in chunks behind stream holds so the host's "
+            "launch rate is out of the figure; LRU, cold start. cpu_baseline.fused_us_per_layer_step is "
             "the oracle's fused step in C on one core with the state in host memory: it "
             "leaves out moving each step's ids to the host and the outputs back, which a "
             "CPU path would pay every layer-step", "runs": runs}
@@ -933,6 +1286,63 @@ def _distinct(np, ids):
 
 def _row(t, l):
     return ctypes.c_void_p(t.data_ptr() + l * t.stride(0) * t.element_size())
+
+
+def _row_off(t, l, i):
+    return ctypes.c_void_p(t.data_ptr() + (l * t.stride(0) + i) * t.element_size())
+
+
+def _oracle_prefetch_sequence(np, snap_np, ids, pred, L, E, S, mk, policy, decay, budget):
+    """Per layer, from the snapshot's state: for each step t, the oracle's prefetch step of
+    pred[t, l] (when pred is given) and then its policy step of ids[t, l], as the prefetch
+    leg's graph orders them for that layer. Returns per-layer n_miss [K], miss pairs, the
+    prefetch step's n_miss and pairs, and the final state."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+
+    K = ids.shape[0]
+
+    def layer(l):
+        s = oracle.State(E, S)
+        for f in ("table", "map_cold", "slot_expert", "slot_stamp", "step", "miss"):
+            getattr(s, f)[:] = snap_np[f][l].ravel()
+        nm = np.zeros(K, np.int32)
+        pn = np.zeros(K, np.int32)
+        pairs, pf_pairs = [], []
+        for t in range(K):
+            if pred is not None:
+                assert s.prefetch(pred[t, l], budget) == 0
+                pn[t] = s.n_miss[0]
+                pf_pairs.append(s.miss[:2 * pn[t]].copy())
+            assert s.manage(ids[t, l], min(E, mk), S, policy, decay) == 0
+            nm[t] = s.n_miss[0]
+            pairs.append(s.miss[:2 * nm[t]].copy())
+        return {"n_miss": nm, "pairs": pairs, "pf_n_miss": pn, "pf_pairs": pf_pairs,
+                "final": {f: getattr(s, f).copy() for f in
+                          ("table", "map_cold", "slot_expert", "slot_stamp", "step")}}
+
+    with ThreadPoolExecutor(max(1, min(16, os.cpu_count() or 1))) as ex:
+        return list(ex.map(layer, range(L)))
+
+
+def _prefetch_matches(np, want, nm, miss, pn, pf_miss, final):
+    """The prefetch leg's GPU record (nm [K, L], miss [K, L, 2S], pn / pf_miss likewise or
+    None, final state fields [L, ...]) against _oracle_prefetch_sequence."""
+    for l, w in enumerate(want):
+        if not np.array_equal(w["n_miss"], nm[:, l]):
+            return False
+        if any(not np.array_equal(p, miss[t, l, :len(p)]) for t, p in enumerate(w["pairs"])):
+            return False
+        if pn is not None:
+            if not np.array_equal(w["pf_n_miss"], pn[:, l]):
+                return False
+            if any(not np.array_equal(p, pf_miss[t, l, :len(p)])
+                   for t, p in enumerate(w["pf_pairs"])):
+                return False
+        if any(not np.array_equal(w["final"][f].ravel(), final[f][l].ravel()) for f in final):
+            return False
+    return True
 
 
 PREFETCH_RUNS = (
@@ -970,7 +1380,7 @@ def _predictions(np, ids_np, W, K, E, q, errors):
 
 
 def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, policy, decay,
-                 W, T, B_exp, chunks, lanes, dev, peak, window=1024,
+                 W, T, B_exp, chunks, lanes, dev, peak, slots, content, bufs, window=1024,
                  compute=(0, 50), runs=PREFETCH_RUNS, pf_chunks=None):
     """Prefetch over trace steps W..T, every run from the same start state (the snapshot
     `snap` taken at step W of the trace pass), as one captured graph per decode step.
@@ -993,7 +1403,13 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     _predictions; accuracy 1.0 is an upper bound no real predictor reaches. Each run is a
     dict of accuracy (absent: no prefetch), lookahead, one_launch (default True), late_fork
     (default False), budget (inserts per prefetch step, default S) and errors ("uniform",
-    the default, or "routed")."""
+    the default, or "routed").
+
+    Checked: every run's per-step n_miss and miss list of each layer's real step and of its
+    prefetch step, and the final state, against the oracle's prefetch and policy steps
+    (oracle/policy.c) called in the order the graph makes them per layer; and, in the first
+    run of each predictor accuracy, every resident slot's bytes at the end, the slots having
+    been re-gathered from the snapshot's residents before the run."""
     K = min(window, T - W)
     i32 = torch.int32
     tt, ll = np.meshgrid(np.arange(K), np.arange(L), indexing="ij")
@@ -1022,6 +1438,29 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     nm_hist = torch.zeros((K, L), dtype=i32, device=dev)
     pf_hist = torch.zeros((K, L), dtype=i32, device=dev)
     pf_miss_hist = torch.zeros((K, L, 2 * S), dtype=i32, device=dev)
+    miss_hist = torch.zeros((K, L, 2 * S), dtype=i32, device=dev)
+    snap_np = {f: snap[f].cpu().numpy() for f in ("table", "map_cold", "slot_expert",
+                                                  "slot_stamp", "step", "miss")}
+    expected = {}  # oracle sequences by (predictor, errors, budget)
+    checks = []
+    slot_checked = set()
+
+    def regather():
+        """Slot bytes consistent with the snapshot: every resident (expert, slot) copied."""
+        rec = torch.zeros((L, 1 + 2 * S), dtype=i32)
+        for l in range(L):
+            se = snap_np["slot_expert"][l]
+            res = np.nonzero(se >= 0)[0]
+            rec[l, 0] = len(res)
+            rec[l, 1:1 + 2 * len(res):2] = torch.as_tensor(se[res])
+            rec[l, 2:2 + 2 * len(res):2] = torch.as_tensor(res.astype(np.int32))
+        rec = rec.to(dev)
+        s0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for l in range(L):
+            if lib.expert_cache_gather(*g_args[l][:18], _row_off(rec, l, 1), _row(rec, l),
+                                       chunks, lanes, s0):
+                raise RuntimeError("re-gather launch failed")
+        torch.cuda.synchronize()
     side = torch.cuda.Stream(dev)
     done = [torch.cuda.Event() for _ in range(L)]
     m_args = [(_row(ids_static, l), 4, mk, E, S, min(E, mk), S, st.row("table", l),
@@ -1093,7 +1532,13 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                                            _predictions(np, ids_np, W, K, E, q, errors))
             if pred is not None:
                 pred_dev = torch.as_tensor(np.ascontiguousarray(pred), device=dev)
+            key = (q, errors if q is not None and q < 1.0 else None,
+                   budget if q is not None else None)
+            check_slots = key[:2] not in slot_checked
+            slot_checked.add(key[:2])
             st.restore(snap)
+            if check_slots:
+                regather()
             pf_nm.zero_()
             pf_hist.zero_()
             torch.cuda.synchronize()
@@ -1109,6 +1554,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                     pred_static.copy_(pred_dev[t], non_blocking=True)
                 g.replay()
                 nm_hist[t].copy_(nm_static, non_blocking=True)
+                miss_hist[t].copy_(st.miss, non_blocking=True)
                 if pred is not None:
                     pf_hist[t].copy_(pf_nm, non_blocking=True)
                     pf_miss_hist[t].copy_(pf_miss, non_blocking=True)
@@ -1117,6 +1563,21 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             elapsed = max(time.perf_counter() - wall0, a.elapsed_time(b) * 1e-3)
             del g
             nm, pn = nm_hist.cpu().numpy(), pf_hist.cpu().numpy()
+            if key not in expected:
+                expected[key] = _oracle_prefetch_sequence(
+                    np, snap_np, ids_np[W:W + K], pred, L, E, S, mk, policy, decay, budget)
+            ok = _prefetch_matches(np, expected[key], nm, miss_hist.cpu().numpy(),
+                                   pn if pred is not None else None,
+                                   pf_miss_hist.cpu().numpy() if pred is not None else None,
+                                   {f: getattr(st, f).cpu().numpy() for f in
+                                    ("table", "map_cold", "slot_expert", "slot_stamp", "step")})
+            slots_ok = None
+            if check_slots:
+                from vllm_expert_cache import traces
+                slots_ok = all(traces.slots_match(slots[l][b], st.slot_expert[l], content[l],
+                                                  b, nb)[0]
+                               for l in range(L) for b, nb in enumerate(bufs))
+            checks.append({"oracle": ok, "slot_bytes": slots_ok})
             used = 0
             if pred is not None:
                 fetched = pf_miss_hist.cpu().numpy()[..., 0::2]
@@ -1148,22 +1609,47 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 f"{f', budget {budget}' if budget < S else ''}")
             log(f"prefetch leg, compute {C} us/layer, predictor {desc}: {ms:.3f} ms/step "
                 f"({base_ms[C] / ms:.3f}x), {int(pn.sum())} prefetched ({used} used), "
-                f"{int(nm.sum())} on the critical path")
+                f"{int(nm.sum())} on the critical path; oracle {'equal' if ok else 'MISMATCH'}"
+                f"{'' if slots_ok is None else ', slot bytes ' + ('equal' if slots_ok else 'MISMATCH')}")
     return {"window_steps": K, "trace_steps": [W, W + K],
             "spin_cycles_per_us": round(cyc_per_us, 1),
             "copy_grid": [pf_chunks or chunks, 1],
             "def": "useful_GBps counts the experts a step needed (critical-path inserts plus "
                    "prefetched experts that were routed), not the partial copies of dropped "
-                   "predictions", "runs": out}
+                   "predictions", "runs": out,
+            "verified": {"oracle_runs": sum(c["oracle"] for c in checks),
+                         "runs": len(checks),
+                         "slot_byte_runs": sum(c["slot_bytes"] is True for c in checks),
+                         "slot_byte_checks": sum(c["slot_bytes"] is not None for c in checks),
+                         "all": all(c["oracle"] and c["slot_bytes"] is not False
+                                    for c in checks),
+                         "def": "per run: each layer's per-step n_miss and miss list (real "
+                                "and prefetch steps) and final state against the oracle's "
+                                "prefetch and policy steps in the graph's per-layer order; "
+                                "in the first run of each predictor, every resident slot's "
+                                "bytes after the run (slots re-gathered from the start "
+                                "state's residents first)"}}
 
 
-def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
+SWEEP_CHUNK = 16  # decode steps per captured graph in the hit-rate sweep
+
+
+def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev, hold):
     """Hit rate per slot budget and policy over the whole trace from a cold start, on the
-    GPU policy kernel: one captured graph of L manage+remap launches per step (no gather;
-    hit rate and gather volume depend only on the policy). Also the graph's time per layer,
-    which is kernel time plus graph node gaps plus the per-step id copy."""
+    GPU policy kernel (no gather: hit rate and gather volume depend only on the policy).
+
+    SWEEP_CHUNK decode steps are captured in one graph of SWEEP_CHUNK x L policy+remap
+    launches, each reading its step's ids from a window buffer and writing its n_miss into a
+    window of the history; per chunk the host copies the window's ids in, replays, and
+    copies the n_miss window out. Chunks are queued behind stream holds, so the graph's time
+    per layer is the policy launches back to back (kernel plus graph node gap), with two
+    small copies per SWEEP_CHUNK steps, not the host's queueing rate."""
     T = ids_np.shape[0]
+    C = SWEEP_CHUNK
     distinct = _distinct(np, ids_np)  # [T, L]
+    Tp = -(-T // C) * C  # padded to whole chunks with empty steps (-1 ids: nothing routed)
+    ids_pad = torch.full((Tp, L, mk), -1, dtype=torch.int32, device=dev)
+    ids_pad[:T].copy_(ids_dev)
     out = []
     for S in w.slots:
         if mk > S:
@@ -1173,43 +1659,34 @@ def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
         for pol_name in w.policies:
             pol = 1 if pol_name == "lfu" else 0
             st = Layers(torch, L, E, S, dev)
-            snap0 = st.snapshot()
-            ids_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+            ids_win = torch.zeros((C, L, mk), dtype=torch.int32, device=dev)
             out_static = torch.zeros((L, mk), dtype=torch.int32, device=dev)
-            nm_static = torch.zeros((L,), dtype=torch.int32, device=dev)
-            nm_hist = torch.zeros((T, L), dtype=torch.int32, device=dev)
-            args_l = [(_row(ids_static, l), 4, mk, E, S, min(E, mk), S, st.row("table", l),
-                       st.row("map_cold", l), st.row("slot_expert", l),
-                       st.row("slot_stamp", l), st.row("routed", l), st.row("step", l),
-                       st.row("miss", l), _row(nm_static, l), pol, decay, _row(out_static, l))
-                      for l in range(L)]
+            nm_win = torch.zeros((C, L), dtype=torch.int32, device=dev)
+            nm_hist = torch.zeros((Tp, L), dtype=torch.int32, device=dev)
+            args_l = [[(_row(ids_win[i], l), 4, mk, E, S, min(E, mk), S, st.row("table", l),
+                        st.row("map_cold", l), st.row("slot_expert", l),
+                        st.row("slot_stamp", l), st.row("routed", l), st.row("step", l),
+                        st.row("miss", l), _row(nm_win[i], l), pol, decay,
+                        _row(out_static, l)) for l in range(L)] for i in range(C)]
 
-            def launch(stream):
-                sp = ctypes.c_void_p(stream.cuda_stream)
-                for l in range(L):
-                    if lib.expert_cache_manage_remap(*args_l[l], sp):
-                        raise RuntimeError("manage launch failed")
-
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                launch(side)
-            torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize()
-            st.restore(snap0)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream())
+                sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(C):
+                    for l in range(L):
+                        if lib.expert_cache_manage_remap(*args_l[i][l], sp):
+                            raise RuntimeError("manage launch failed")
             torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            for t in range(T):
-                ids_static.copy_(ids_dev[t], non_blocking=True)
+
+            def enqueue(k):
+                ids_win.copy_(ids_pad[k * C:(k + 1) * C], non_blocking=True)
                 g.replay()
-                nm_hist[t].copy_(nm_static, non_blocking=True)
-            b.record()
-            torch.cuda.synchronize()
-            nm = nm_hist.cpu().numpy()
+                nm_hist[k * C:(k + 1) * C].copy_(nm_win, non_blocking=True)
+
+            sec = sum(x[2] for x in hold.time(0, Tp // C, enqueue, chunk=4))
+            nm = nm_hist[:T].cpu().numpy()
+            # a padded step routes nothing, so it inserts nothing; its launches are timed
+            # with the rest (at most C - 1 steps of T)
             per_layer = 1.0 - nm.sum(0) / distinct.sum(0)
             out.append({"slots": S, "policy": pol_name, "steps": T,
                         "hit_rate": round(float(1.0 - nm.sum() / distinct.sum()), 5),
@@ -1217,7 +1694,7 @@ def hit_rate_sweep(torch, np, lib, w, ids_np, ids_dev, L, E, mk, decay, dev):
                         "per_layer_hit_rate_max": round(float(per_layer.max()), 5),
                         "inserts": int(nm.sum()),
                         "gather_volume_GB": round(float(nm.sum()) * w.bytes_per_expert / 1e9, 2),
-                        "graph_us_per_layer": round(a.elapsed_time(b) * 1e3 / (T * L), 3)})
+                        "graph_us_per_layer": round(sec * 1e6 / (Tp * L), 3)})
             log(f"hit-rate sweep: S={S} {pol_name}: {out[-1]['hit_rate']} "
                 f"(layers {out[-1]['per_layer_hit_rate_min']}..{out[-1]['per_layer_hit_rate_max']}), "
                 f"{out[-1]['gather_volume_GB']} GB, {out[-1]['graph_us_per_layer']} us/layer")

@@ -39,11 +39,13 @@ def _words(s: oracle.State) -> np.ndarray:
                            s.step.view(np.int32)])
 
 
-@pytest.mark.parametrize("entry", ENTRIES)
-@pytest.mark.parametrize("E,S,mk", SHAPES, ids=lambda v: str(v))
+# expert_cache_fused takes at most 1024 experts, so it runs on the first two shapes only
+CASES = [(entry, *shape) for shape in SHAPES for entry in ENTRIES
+         if not (entry == "fused" and shape[0] > 1024)]
+
+
+@pytest.mark.parametrize("entry,E,S,mk", CASES, ids=lambda v: str(v))
 def test_pending_installs_settle_like_the_oracle(entry, E, S, mk):
-    if entry == "fused" and E > 1024:
-        pytest.skip("expert_cache_fused takes at most 1024 experts")
     rng = np.random.default_rng(E * 31 + S)
     policy = LRU if entry == "fused" else LFU
     decay = 0 if entry == "fused" else 4

@@ -16,10 +16,13 @@ captured in HIP graphs so that host launch cost is out of the picture:
     (4 layers, 128 slots, 128 ids per step).
 
 Each test prints one "speed:" line per figure (run pytest with -s to see them). The byte
-checks are the gate. The times are reported, not asserted: EC_SPEED_ASSERT=1 turns on a
-regression guard (this library not slower than the reference beyond a 10 % noise margin),
-for a quiet machine and not under a profiler, whose per-dispatch cost swamps kernels of a
-few microseconds.
+checks come first. Then a regression guard: this library not slower than the reference
+beyond a 10 % noise margin. By default it guards the comparisons where this library leads
+clearly (the policy step at the reference's timing shape, the decode loops of the 4.7 MB
+and 352 MB experts, the fused kernel); where both sides run at the host link's rate (the
+gathers of the reference's shapes, the batch-4 and 44 MB decode loops) the times are
+reported only. EC_SPEED_ASSERT=1 guards every comparison, EC_SPEED_ASSERT=0 none (for a
+run under a profiler, whose per-dispatch cost swamps kernels of a few microseconds).
 """
 from __future__ import annotations
 
@@ -41,15 +44,16 @@ REF_CHUNKS, REF_LANES = 16, 64      # vllm_expert_cache/cache.py:96-97 of the re
 REF_SIZES = (819200, 409600, 51200, 640, 25600, 2560)   # tests/test_policy.py:237
 
 
-SPEED_ASSERT = os.environ.get("EC_SPEED_ASSERT", "0") == "1"
-# a regression guard, not the measurement (the timings are printed): the closest case, the
-# 44 MB experts where both sides run at the link's rate, is a tie, so leave room for noise
+SPEED_ASSERT = os.environ.get("EC_SPEED_ASSERT")  # "1": every comparison, "0": none
+# a regression guard, not the measurement (the timings are printed); ties at the link's rate
+# get room for noise
 MARGIN = 1.10
 
 
-def _not_slower(this: float, reference: float) -> bool:
-    """Times (lower is better): this within MARGIN of the reference, unless disabled."""
-    return not SPEED_ASSERT or this <= reference * MARGIN
+def _not_slower(this: float, reference: float, clear_lead: bool = True) -> bool:
+    """Times (lower is better): this within MARGIN of the reference, where guarded."""
+    guarded = SPEED_ASSERT == "1" or (SPEED_ASSERT != "0" and clear_lead)
+    return not guarded or this <= reference * MARGIN
 
 
 def _ref():
@@ -179,7 +183,7 @@ def test_gather_vs_reference(store_512, n):
     gbs = {k: n * per_expert / (v * 1e-6) / 1e9 for k, v in us.items()}
     _say(f"gather {n:2d} x {per_expert} B: reference {us['reference']:.1f} us "
          f"({gbs['reference']:.1f} GB/s), this {us['this']:.1f} us ({gbs['this']:.1f} GB/s)")
-    assert _not_slower(us["this"], us["reference"])
+    assert _not_slower(us["this"], us["reference"], clear_lead=False)
 
 
 # ---- the 48-layer-e128 decode loop through each side's refresh -----------------------------
@@ -295,7 +299,8 @@ def test_decode_loop_vs_reference(name, S, L, T):
     _say(f"decode loop {workload} ({L} layers x {T} steps, S={S}, LFU, {inserts} inserts, "
          f"{gb:.1f} GB): reference {r['ms']:.1f} ms ({gb / r['ms'] * 1e3:.1f} GB/s), "
          f"this {m['ms']:.1f} ms ({gb / m['ms'] * 1e3:.1f} GB/s)")
-    assert _not_slower(m["ms"], r["ms"])
+    assert _not_slower(m["ms"], r["ms"],
+                       clear_lead=name in ("48-layer-e128", "8-layer-e8-bf16"))
 
 
 # ---- expert_cache_fused: the LRU step plus both moe_align_block_size outputs ---------------

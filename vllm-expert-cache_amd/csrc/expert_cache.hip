@@ -14,56 +14,11 @@
 namespace ec {
 namespace {
 
-// Gather tile: 256 lanes x 2 vectors = 8 KB per workgroup iteration, loads non-temporal
-// (host rows are streamed once), stores default so the fresh slot stays in cache for the
-// GEMM that reads it next. Measured on MI355X over PCIe Gen5: the host link saturates at
-// ~128-256 KB in flight (its bandwidth-delay product); far more in flight at once (every
-// tile of an expert issued together) drops a 4.7 MB expert from ~54.5 to ~41 GB/s. So the
-// caller's grid should be small (32 workgroups x 8 KB = 256 KB) and the tiles stream
-// through the expert in order, each workgroup taking every grid-th tile.
-constexpr int kGatherUnroll = 2;
-
 // [p, p + pn) and [q, q + qn) share a byte
 bool ranges_meet(const void* p, long long pn, const void* q, long long qn) {
   const long long a = (long long)reinterpret_cast<uintptr_t>(p);
   const long long b = (long long)reinterpret_cast<uintptr_t>(q);
   return pn > 0 && qn > 0 && a < b + qn && b < a + pn;
-}
-
-// The gather's launch arguments from the six (dst, src, bytes) triples: the checks of
-// kernels/expert_cache.hip:631-634, then the buffers with a repeated (dst, src, bytes) -- the
-// caller's padding of a short list -- dropped, since they would copy the same bytes to the
-// same place, and each workgroup's stride through the step's (miss, tile) space.
-bool gather_plan(void* const (&dst)[kGatherBufs], const void* const (&src)[kGatherBufs],
-                 const long (&bytes)[kGatherBufs], int chunks, int lanes, GatherArgs& g) {
-  for (int i = 0; i < kGatherBufs; i++)
-    if (bytes[i] <= 0 || bytes[i] % 16) return false;
-  if (chunks <= 0 || lanes <= 0) return false;
-  constexpr long long kTile = (long long)kGatherThreads * kGatherUnroll;
-  g.nbuf = 0;
-  g.tile0[0] = 0;
-  for (int i = 0; i < kGatherBufs; i++) {
-    bool dup = false;
-    for (int k = 0; k < i; k++)
-      dup = dup || (dst[k] == dst[i] && src[k] == src[i] && bytes[k] == bytes[i]);
-    if (dup) continue;
-    const int b = g.nbuf++;
-    g.dst[b] = static_cast<u32x4*>(dst[i]);
-    g.src[b] = static_cast<const u32x4*>(src[i]);
-    g.vec[b] = bytes[i] / 16;
-    g.tile0[b + 1] = g.tile0[b] + (g.vec[b] + kTile - 1) / kTile;
-  }
-  for (int b = g.nbuf; b < kGatherBufs; b++) {
-    g.dst[b] = nullptr;
-    g.src[b] = nullptr;
-    g.vec[b] = 0;
-    g.tile0[b + 1] = g.tile0[b];
-  }
-  g.per = g.tile0[g.nbuf];
-  const long long nblk = (long long)chunks * lanes;
-  g.jstep = g.per > 0 ? nblk / g.per : 0;
-  g.rstep = g.per > 0 ? nblk % g.per : 0;
-  return true;
 }
 
 bool manage_args_bad(int E, int S, int max_inserts, int policy) {

@@ -105,12 +105,10 @@ __device__ __forceinline__ void tile_store(const GatherTile& t, const u32x4 (&v)
 // without one. Tiles already loaded are still stored: a dropped slot is empty, or gets
 // another expert whose own copy the caller orders after this kernel.
 template <int U, bool NT_LOAD, bool NT_STORE, bool LIVE>
-__global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
-                                                           const int* __restrict__ miss,
-                                                           const int* __restrict__ n_miss,
-                                                           const int* slot_expert) {
+__device__ __forceinline__ void gather_walk(const GatherArgs& g, const int* __restrict__ miss,
+                                            const int* __restrict__ n_miss,
+                                            const int* slot_expert, long long t0) {
   const long long per = g.per;
-  const long long t0 = (long long)blockIdx.y * gridDim.x + blockIdx.x;
   // The miss list is read only below n_miss, as kernels/expert_cache.hip:294-298 reads it:
   // a caller with no insert capacity (max_inserts = 0) may pass an empty list.
   const int nm = n_miss[0];
@@ -166,6 +164,64 @@ __global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
     }
   }
   if (have) tile_store<U, NT_STORE>(cur, v);
+}
+
+template <int U, bool NT_LOAD, bool NT_STORE, bool LIVE>
+__global__ __launch_bounds__(kGatherThreads) void gather_k(GatherArgs g,
+                                                           const int* __restrict__ miss,
+                                                           const int* __restrict__ n_miss,
+                                                           const int* slot_expert) {
+  gather_walk<U, NT_LOAD, NT_STORE, LIVE>(g, miss, n_miss, slot_expert,
+                                          (long long)blockIdx.y * gridDim.x + blockIdx.x);
+}
+
+// Gather tile: 256 lanes x 2 vectors = 8 KB per workgroup iteration, loads non-temporal
+// (host rows are streamed once), stores default so the fresh slot stays in cache for the
+// GEMM that reads it next. Measured on MI355X over PCIe Gen5: the host link saturates at
+// ~128-256 KB in flight (its bandwidth-delay product); far more in flight at once (every
+// tile of an expert issued together) drops a 4.7 MB expert from ~54.5 to ~41 GB/s. So the
+// caller's grid should be small (32 workgroups x 8 KB = 256 KB) and the tiles stream
+// through the expert in order, each workgroup taking every grid-th tile. Fewer, wider
+// workgroups with the same bytes in flight are slower (16 x 16 KB and 8 x 32 KB took 1.26x
+// and 2.3x as long per decode step): one compute unit keeps only so many host reads in
+// flight, so the reads must spread over many.
+constexpr int kGatherUnroll = 2;
+
+// The gather's launch arguments from the six (dst, src, bytes) triples: the checks of
+// kernels/expert_cache.hip:631-634, then the buffers with a repeated (dst, src, bytes) -- the
+// caller's padding of a short list -- dropped, since they would copy the same bytes to the
+// same place, and each workgroup's stride through the step's (miss, tile) space.
+inline bool gather_plan(void* const (&dst)[kGatherBufs], const void* const (&src)[kGatherBufs],
+                        const long (&bytes)[kGatherBufs], int chunks, int lanes,
+                        GatherArgs& g) {
+  for (int i = 0; i < kGatherBufs; i++)
+    if (bytes[i] <= 0 || bytes[i] % 16) return false;
+  if (chunks <= 0 || lanes <= 0) return false;
+  constexpr long long kTile = (long long)kGatherThreads * kGatherUnroll;
+  g.nbuf = 0;
+  g.tile0[0] = 0;
+  for (int i = 0; i < kGatherBufs; i++) {
+    bool dup = false;
+    for (int k = 0; k < i; k++)
+      dup = dup || (dst[k] == dst[i] && src[k] == src[i] && bytes[k] == bytes[i]);
+    if (dup) continue;
+    const int b = g.nbuf++;
+    g.dst[b] = static_cast<u32x4*>(dst[i]);
+    g.src[b] = static_cast<const u32x4*>(src[i]);
+    g.vec[b] = bytes[i] / 16;
+    g.tile0[b + 1] = g.tile0[b] + (g.vec[b] + kTile - 1) / kTile;
+  }
+  for (int b = g.nbuf; b < kGatherBufs; b++) {
+    g.dst[b] = nullptr;
+    g.src[b] = nullptr;
+    g.vec[b] = 0;
+    g.tile0[b + 1] = g.tile0[b];
+  }
+  g.per = g.tile0[g.nbuf];
+  const long long nblk = (long long)chunks * lanes;
+  g.jstep = g.per > 0 ? nblk / g.per : 0;
+  g.rstep = g.per > 0 ? nblk % g.per : 0;
+  return true;
 }
 
 }  // namespace ec

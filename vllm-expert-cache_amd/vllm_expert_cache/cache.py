@@ -112,25 +112,22 @@ class ExpertSlotCache:
         self.E = int(num_experts)
         self.S = int(num_slots)
 
-        self.slots: dict[str, torch.Tensor] = {}
-        self.skipped: list[str] = []
-        ragged = []
-        for n in self.names:
-            full = getattr(owner, n).data
-            # The gather moves 16-byte vectors. A ragged weight the GEMM reads directly is
-            # fatal; a ragged auxiliary tensor is left unmirrored and the caller's leak check
-            # decides whether the quantisation config actually indexes it per expert.
-            nbytes = _bytes_per_expert(full)
-            if nbytes % 16:
-                (ragged if n in required else self.skipped).append(
-                    f"{n}{tuple(full.shape)}={nbytes}B")
-                continue
-            self.slots[n] = torch.empty((self.S,) + tuple(full.shape[1:]), dtype=full.dtype,
-                                        device=device)
-        if ragged:
+        # The gather moves 16-byte vectors, so a slab of another size cannot be mirrored. A
+        # required one (a weight the GEMM reads directly) is fatal; any other is left
+        # unmirrored, and the caller's leak check decides whether the quantisation config
+        # actually indexes it per expert.
+        fulls = {n: getattr(owner, n).data for n in self.names}
+        odd = {n: f"{n}{tuple(t.shape)}={_bytes_per_expert(t)}B" for n, t in fulls.items()
+               if _bytes_per_expert(t) % 16}
+        fatal = [desc for n, desc in odd.items() if n in required]
+        if fatal:
             raise ValueError("per-expert slab must be a multiple of 16 bytes, but these are "
-                             "not: " + ", ".join(ragged))
-        self.names = [n for n in self.names if n in self.slots]
+                             "not: " + ", ".join(fatal))
+        self.skipped: list[str] = [desc for n, desc in odd.items() if n not in required]
+        self.names = [n for n in self.names if n not in odd]
+        self.slots: dict[str, torch.Tensor] = {
+            n: torch.empty((self.S,) + tuple(fulls[n].shape[1:]), dtype=fulls[n].dtype,
+                           device=device) for n in self.names}
 
         # What the layer's attributes are rebound to during a cached step; built once so
         # graph capture sees fixed storage.
