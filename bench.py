@@ -25,10 +25,17 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
   roofline     the gather kernel: achieved host->HBM GB/s (algorithmic bytes / kernel time,
                HIP events on the launch stream over segments of the timed steps) against
                the measured host->device link peak; roofline.steady_state is the same over
-               segments of the steady-state window
-  manage_remap_us_per_layer   cost of the fused policy+remap kernel per layer inside the
-               decode graph (hit-rate pass at this budget and policy, whole trace); the
-               event-bracketed figure, an upper bound, is manage_remap_us_per_layer_events
+               segments of the steady-state window. frac_trace_pass / frac_steady_state:
+               the same rate inside the decode graph by node substitution (decode_chain);
+               frac_*_kernel: by clock stamps inside the kernels (decode_chain.stamps)
+  manage_remap_us_per_layer   what the fused policy+remap launch adds to the decode graph
+               per layer over the trace pass: the graph's time minus that of the same graph
+               with only its gathers (decode_chain), no events or profiler in the chain;
+               manage_remap_kernel_us_in_chain is the kernel's own run time there (clock
+               stamps), manage_remap_us_per_layer_policy_graph a graph of the policy
+               launches alone, and manage_remap_us_per_layer_events the event-bracketed
+               upper bound
+  decode_chain the decode graph's per-node costs by substitution and by clock stamps
   hit_rate     1 - inserts / distinct routed experts over the timed steps
   hit_rate_sweep  every slot budget x LFU/LRU over the whole trace from a cold start, with
                the per-layer range
@@ -42,7 +49,7 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
                compute and with a 50 us-per-layer compute stand-in; predictors of accuracy
                1.0 (the true routing: an upper bound) and 0.8 (each id wrong with
                probability 0.2, the wrong guess a uniformly random expert or one the layer
-               routes elsewhere in the trace), one and two layers ahead, the prefetch step
+               routes elsewhere in the trace), one to four layers ahead, the prefetch step
                launched on its own (expert_cache_prefetch) or inside the policy launch
                (expert_cache_manage_remap_prefetch), the copy forked after the policy launch
                or after the layer's gather, and an insert budget of one
@@ -134,14 +141,19 @@ def parse():
                    help="experts per layer of a --routes trace (default: the workload's)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: 16 gathers of one expert each (plain, then "
-                        "live), 128 policy steps and 8 plain device copies of 64 MiB (the "
-                        "counter calibration), nothing else")
+                        "live), 128 policy steps of one layer, 96 decode steps of every layer "
+                        "launched eagerly, and 8 plain device copies of 64 MiB (the counter "
+                        "calibration), nothing else")
     return p.parse_args()
+
+
+CHAIN_STEPS = 96  # decode steps of the traffic probe's eager decode loop
 
 
 def traffic_probe(args):
     """Known work for the counter runs: 16 one-expert gathers, the same 16 through the live
-    gather, 128 policy+remap steps of one layer, and 8 plain device copies whose FETCH_SIZE /
+    gather, 128 policy+remap steps of one layer back to back, the decode loop of every layer
+    launched eagerly over CHAIN_STEPS steps, and 8 plain device copies whose FETCH_SIZE /
     WRITE_SIZE per byte calibrate the kernels' per-launch counters into bytes."""
     import torch
 
@@ -193,6 +205,38 @@ def traffic_probe(args):
             st.row("routed", 0), st.row("step", 0), st.row("miss", 0),
             ctypes.c_void_p(nm.data_ptr()), 1, 64, ctypes.c_void_p(out.data_ptr()), s_ptr)
         assert rc == 0
+    # the decode loop, launched eagerly: every layer of the workload over CHAIN_STEPS trace
+    # steps from a cold start, per layer the policy+remap step and then the gather of its
+    # misses, as the decode graph orders them (every layer reads the one host store above;
+    # each has its own slots). The policy counters of the last 32 steps are its in-chain
+    # figures, beside the back-to-back ones of the single layer above.
+    import numpy as np
+
+    L, T = w.layers, CHAIN_STEPS
+    ids = torch.as_tensor(np.stack([traces.routing(w, l, T) for l in range(L)], axis=1),
+                          device=dev)
+    st = Layers(torch, L, E, S, dev)
+    nm = torch.zeros(L, dtype=torch.int32, device=dev)
+    out = torch.zeros((L, mk), dtype=torch.int32, device=dev)
+    lslots = [[torch.empty(S * b, dtype=torch.uint8, device=dev) for b in bufs]
+              for _ in range(L)]
+    for t in range(T):
+        for l in range(L):
+            rc = lib.expert_cache_manage_remap(
+                ctypes.c_void_p(ids[t, l].data_ptr()), 4, mk, E, S, min(E, mk), S,
+                st.row("table", l), st.row("map_cold", l), st.row("slot_expert", l),
+                st.row("slot_stamp", l), st.row("routed", l), st.row("step", l),
+                st.row("miss", l), ctypes.c_void_p(nm[l:].data_ptr()), 1, 64,
+                ctypes.c_void_p(out[l].data_ptr()), s_ptr)
+            g = []
+            for i in range(6):
+                j = min(i, len(bufs) - 1)
+                g += [ctypes.c_void_p(lslots[l][j].data_ptr()), a[3 * j + 1], a[3 * j + 2]]
+            rc |= lib.expert_cache_gather(*g, st.row("miss", l),
+                                          ctypes.c_void_p(nm[l:].data_ptr()),
+                                          args.chunks or DEFAULT_CHUNKS,
+                                          args.lanes or DEFAULT_LANES, s_ptr)
+            assert rc == 0
     n = 64 << 20
     src = torch.ones(n, dtype=torch.uint8, device=dev)
     dst = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -201,7 +245,8 @@ def traffic_probe(args):
     torch.cuda.synchronize()
     print(json.dumps({"gather_launches": 16, "gather_live_launches": 16,
                       "gather_bytes_per_launch": sum(bufs),
-                      "manage_remap_launches": 128, "copy_launches": 8,
+                      "manage_remap_launches": 128, "decode_loop_layers": L,
+                      "decode_loop_steps": T, "copy_launches": 8,
                       "copy_bytes_per_launch": n}), flush=True)
 
 
@@ -878,6 +923,8 @@ def _stamps_lib():
         f.argtypes = SIGNATURES[base][:-1] + [P, P]  # ... row(s), stream
     h.stamped_empty.restype = ctypes.c_int
     h.stamped_empty.argtypes = [P, P]
+    h.stamped_clock_khz.restype = ctypes.c_int
+    h.stamped_clock_khz.argtypes = [ctypes.c_int]
     return h
 
 
@@ -906,18 +953,33 @@ def chain_stamps(torch, np, hold, m_args, g_args, st, snap, final, ids_dev, ids_
     def rp(l, k):
         return ctypes.c_void_p(rows.data_ptr() + (l * (1 + grid) + k) * 16)
 
-    # the clock's rate: two stamped empty kernels around a spin, against HIP events
+    # the clock's rate: two stamped empty kernels around a 200 ms spin, timed by HIP events
+    # and by the host's clock (which the stamps are converted with: the host's launch and
+    # synchronisation add ~0.01 %), beside the rate the device reports
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    # a first launch loads the library's code object (milliseconds on the host), which must
+    # not fall inside the interval
+    assert sl.stamped_empty(rp(0, 0), s0) == 0
     torch.cuda.synchronize()
+    h0 = time.perf_counter()
     a.record()
     assert sl.stamped_empty(rp(0, 0), s0) == 0
-    torch.cuda._sleep(int(50000 * hold.cyc_per_us))
+    torch.cuda._sleep(int(200000 * hold.cyc_per_us))
     assert sl.stamped_empty(rp(1, 0), s0) == 0
     b.record()
     torch.cuda.synchronize()
+    wall_s = time.perf_counter() - h0
     r = rows.cpu().numpy()
-    mhz = (r[1, 0, 0] - r[0, 0, 0]) / (a.elapsed_time(b) * 1e3)
+    ticks = float(r[1, 0, 0] - r[0, 0, 0])
+    mhz = ticks / (wall_s * 1e6)
+    clock = {"MHz": round(mhz, 3), "MHz_by_events": round(ticks / (a.elapsed_time(b) * 1e3), 3),
+             "MHz_reported": sl.stamped_clock_khz(0) / 1e3,
+             "events_over_wall": round(a.elapsed_time(b) * 1e-3 / wall_s, 5),
+             "def": "stamp ticks between two stamped kernels around a 200 ms spin, over the "
+                    "host's wall time of the interval (MHz, used to convert the stamps) and "
+                    "over HIP events' elapsed time (MHz_by_events); MHz_reported is the "
+                    "device's hipDeviceAttributeWallClockRate"}
 
     def capture(policy_only):
         g = torch.cuda.CUDAGraph()
@@ -932,7 +994,7 @@ def chain_stamps(torch, np, hold, m_args, g_args, st, snap, final, ids_dev, ids_
         torch.cuda.synchronize()
         return g
 
-    out = {"clock_MHz": round(float(mhz), 2)}
+    out = {"clock_MHz": round(float(mhz), 3), "clock": clock}
     for name in ("chain", "policy_only"):
         g = capture(name == "policy_only")
         st.restore(snap)
@@ -1351,6 +1413,8 @@ PREFETCH_RUNS = (
     {"accuracy": 1.0, "lookahead": 1},
     {"accuracy": 1.0, "lookahead": 1, "late_fork": True},
     {"accuracy": 1.0, "lookahead": 2},
+    {"accuracy": 1.0, "lookahead": 3},
+    {"accuracy": 1.0, "lookahead": 4},
     {"accuracy": 0.8, "lookahead": 1},
     {"accuracy": 0.8, "lookahead": 1, "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2},
@@ -1721,16 +1785,26 @@ def _traffic():
 
 
 def _manage_counters():
-    """Hardware counters per policy+remap call (rocprofv3, calibrated), from the committed
-    profile summary; None if absent."""
+    """Hardware counters per policy+remap call (rocprofv3, calibrated), back to back and in
+    the decode loop, from the committed profile summary; None if absent."""
     p = ROOT / "profiles" / "manage_k-counters-48-layer-e128.json"
     try:
-        t = json.loads(p.read_text())["per_call"]
+        j = json.loads(p.read_text())
+        t, c = j["per_call"], j["in_chain"]
     except (OSError, ValueError, KeyError):
         return None
-    return {"hbm_bytes_read": t["hbm_fetch_bytes"], "hbm_bytes_written": t["hbm_write_bytes"],
-            "hbm_GBps": t["hbm_GBps"], "lds_instructions": t["SQ_INSTS_LDS"],
-            "lds_GBps_estimate": t["lds_GBps_estimate"], "duration_us": t["duration_us"],
+    return {"hbm_bytes_read": c["hbm_fetch_bytes"], "hbm_bytes_written": c["hbm_write_bytes"],
+            "hbm_GBps": c["hbm_GBps"], "lds_instructions": c["SQ_INSTS_LDS"],
+            "lds_GBps_estimate": c["lds_GBps_estimate"],
+            "kernel_us": c["kernel_us_by_clock_stamps"],
+            "wave_cycles": c["SQ_WAVE_CYCLES"],
+            "back_to_back": {"hbm_bytes_read": t["hbm_fetch_bytes"],
+                             "hbm_bytes_written": t["hbm_write_bytes"],
+                             "wave_cycles": t["SQ_WAVE_CYCLES"],
+                             "profiler_duration_us": t["duration_us"]},
+            "profiler_duration_us_in_chain": c["duration_us"],
+            "def": "per call in the decode loop (in_chain of the source); GB/s over the "
+                   "kernel's own run time in the decode graph (clock stamps)",
             "source": f"profiles/{p.name}"}
 
 

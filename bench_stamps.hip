@@ -12,6 +12,7 @@
 //   stamped_manage_remap  expert_cache_manage_remap (int32 ids, E <= 4096) + one row
 //   stamped_gather        expert_cache_gather + one row per workgroup (chunks x lanes rows)
 //   stamped_empty         an empty kernel + one row: the chain's floor
+//   stamped_clock_khz     the nominal rate of the stamps' clock, as the device reports it
 #include <hip/hip_runtime.h>
 
 #include "vllm-expert-cache_amd/csrc/gather.h"
@@ -140,6 +141,13 @@ int stamped_empty(unsigned long long* row, hipStream_t stream) {
   if (row == nullptr) return -1;
   hipLaunchKernelGGL(stamped_empty_k, dim3(1), dim3(kWave), 0, stream, row);
   return (int)hipGetLastError();
+}
+
+// The device's nominal rate of the clock the stamps read, in kHz (-1 if not reported).
+int stamped_clock_khz(int device) {
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, device) != hipSuccess) return -1;
+  return v;
 }
 
 }  // extern "C"
