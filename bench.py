@@ -671,6 +671,8 @@ def main():
         "manage_remap_def": manage_def,
         "manage_remap_us_per_layer_steady_state":
             None if chain is None else chain["steady_state"]["manage_remap_us_per_layer"],
+        "manage_remap_substitution_noise_us":
+            None if chain is None else chain["trace_pass"]["noise_us_per_layer"],
         "manage_remap_over_empty_node_us":
             None if chain is None else chain["trace_pass"]["manage_remap_over_empty_node_us"],
         "empty_node_in_chain_us":
@@ -814,6 +816,8 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
       empty+gather per layer an empty kernel node in place of the policy launch, then the
                    same gather
       policy       per layer only the policy+remap launch
+    The gathers-only variant is replayed a second time; the two replays' difference per
+    layer-step (noise_us_per_layer) is the scale below which a difference means nothing.
 
     Every variant copies the step's routing ids and recorded miss lists into its inputs
     before the replay, so the per-step copies cancel in the differences:
@@ -852,8 +856,11 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
             if lib.expert_cache_manage_remap(*m_args[l], s):
                 raise RuntimeError("policy launch failed")
 
-    variants = {"gathers": capture(gathers), "empty+gather": capture(
-        lambda s: gathers(s, empty=True)), "policy": capture(policy), "full": graph}
+    g_only = capture(gathers)
+    # the gathers-only variant runs twice: the two runs' difference is the substitution's
+    # noise (the host link's rate varies a little from pass to pass)
+    variants = {"gathers": g_only, "empty+gather": capture(lambda s: gathers(s, empty=True)),
+                "policy": capture(policy), "full": graph, "gathers_again": g_only}
     times = {}
     for name, g in variants.items():
         def enqueue(t, g=g):
@@ -867,7 +874,8 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
         log(f"decode chain, {name}: {sum(x[2] for x in times[name]):.4f} s over steps "
             f"{W}..{TP}")
     rerun_equal = all(torch.equal(getattr(st, f), final[f]) for f in st.fields)
-    for name in ("gathers", "empty+gather", "policy"):
+    del g_only
+    for name in ("gathers", "empty+gather", "policy", "gathers_again"):
         del variants[name]
 
     def window(lo):
@@ -879,6 +887,7 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
         return {"trace_steps": [lo, TP],
                 "ms_per_step": round(1e3 * t["full"] / n, 4),
                 "manage_remap_us_per_layer": round((t["full"] - t["gathers"]) * per, 3),
+                "noise_us_per_layer": round(abs(t["gathers_again"] - t["gathers"]) * per, 3),
                 "empty_node_us": round((t["empty+gather"] - t["gathers"]) * per, 3),
                 "manage_remap_over_empty_node_us":
                     round((t["full"] - t["empty+gather"]) * per, 3),
@@ -899,7 +908,8 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
            "def": chain_costs.__doc__.split("\n\n")[1].strip()}
     tp, ss = out["trace_pass"], out["steady_state"]
     log(f"decode chain over steps {W}..{TP}: policy+remap {tp['manage_remap_us_per_layer']} "
-        f"us/layer (empty node {tp['empty_node_us']}, policy-only graph "
+        f"us/layer (noise {tp['noise_us_per_layer']}, empty node {tp['empty_node_us']}, "
+        f"policy-only graph "
         f"{tp['policy_graph_us_per_layer']}), gather {tp['gather_GBps']} GB/s "
         f"({tp['gather_frac']}); steady state from {late0}: policy+remap "
         f"{ss['manage_remap_us_per_layer']} us/layer, gather {ss['gather_GBps']} GB/s "
