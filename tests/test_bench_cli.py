@@ -55,3 +55,61 @@ def test_prefetch_predictions_and_segment_spread():
         starts = bench._spread(lo, hi, n, length)
         assert starts == sorted(set(starts)) and len(starts) <= max(1, n)
         assert all(lo <= s and (s + length <= hi or s == lo) for s in starts)
+
+
+def test_committed_profiles_feed_the_bench_line():
+    """The counter summaries the JSON line quotes (roofline.traffic, manage_remap_counters)
+    load, and their figures hang together: traffic is fetch plus write per one-expert
+    launch, within a few percent of the algorithmic bytes."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    t, m = bench._traffic(), bench._manage_counters()
+    assert t is not None and m is not None
+    assert t["bytes_per_launch"] == t["fetch_bytes_per_miss"] + t["write_bytes_per_miss"]
+    assert t["write_bytes_per_miss"] == t["algorithmic_bytes_per_miss"] == 4732928
+    assert 1.0 <= t["fetch_over_algorithmic"] < 1.05
+    assert m["hbm_bytes_read"] > 0 and m["hbm_bytes_written"] > 0 and m["kernel_us"] > 0
+    # GB/s over the stamped kernel time
+    assert abs(m["hbm_GBps"] - (m["hbm_bytes_read"] + m["hbm_bytes_written"]) /
+               (m["kernel_us"] * 1e3)) < 0.05
+
+
+def test_committed_bench_lines_are_verified_runs():
+    """Every bench JSON line kept under profiles/ is a run of this bench that verified itself
+    (slot bytes and the oracle's per-step miss lists and final state) and reports a gather
+    fraction no larger than the link peak it measured."""
+    import json
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    files = sorted((ROOT / "profiles").glob("bench-*.json"))
+    assert files
+    for f in files:
+        rec = json.loads(f.read_text())
+        line = rec["line"]
+        assert rec["command"].startswith("python3 bench.py"), f.name
+        assert line["metric"] == bench.METRIC
+        assert line["verified"]["all"] is True, f.name
+        for k in ("slot_bytes", "state", "n_miss_per_step", "miss_lists_per_step"):
+            assert line["verified"][k] is True, (f.name, k)
+        assert 0.5 < line["roofline"]["frac"] <= 1.0, f.name
+        assert f.name == f"bench-{line['config']['workload']}.json" or \
+            f.name.startswith(f"bench-{line['config']['workload']}-"), f.name
+
+
+def test_stamps_library_exports():
+    """bench_stamps.so, when built, exports the stamped kernels' entry points the bench
+    binds."""
+    import ctypes
+
+    import pytest
+
+    path = ROOT / "bench_stamps.so"
+    if not path.is_file():
+        pytest.skip("bench_stamps.so not built (run __graft_entry__.build())")
+    h = ctypes.CDLL(str(path))
+    for name in ("stamped_manage_remap", "stamped_gather", "stamped_empty",
+                 "stamped_clock_khz"):
+        assert hasattr(h, name), name
