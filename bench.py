@@ -22,12 +22,15 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
   value        gathered bytes / wall time of the timed steps (GB/s), sources in host memory
   verified     the checks above, with what each covered
   trace_pass   whole-job GB/s, ms/step and hit rate over steps W..4096
-  roofline     the gather kernel: achieved host->HBM GB/s (algorithmic bytes / kernel time,
-               HIP events on the launch stream over segments of the timed steps) against
-               the measured host->device link peak; roofline.steady_state is the same over
-               segments of the steady-state window. frac_trace_pass / frac_steady_state:
-               the same rate inside the decode graph by node substitution (decode_chain);
-               frac_*_kernel: by clock stamps inside the kernels (decode_chain.stamps)
+  roofline     the gather kernel against the measured host->device link peak: achieved
+               host->HBM GB/s over the timed steps = algorithmic bytes / what the gather
+               launches add to the decode graph's time (HIP events on the launch stream,
+               node substitution: decode_chain.timed); achieved_events brackets every launch
+               with HIP events instead (an upper bound on its time), and
+               roofline.steady_state is that over segments of the steady-state window.
+               frac_trace_pass / frac_steady_state: the substitution rate over the trace
+               pass and its second half; frac_*_kernel: by clock stamps inside the kernels
+               (decode_chain.stamps)
   manage_remap_us_per_layer   what the fused policy+remap launch adds to the decode graph
                per layer over the trace pass: the graph's time minus that of the same graph
                with only its gathers (decode_chain), no events or profiler in the chain;
@@ -583,7 +586,7 @@ def main():
     # ---- the decode chain's per-node costs, by substitution --------------------------------
     chain = None if args.no_chain else chain_costs(
         torch, lib, hold, graph, M_ARGS, gather_args, st, snaps[W], final, ids_dev,
-        ids_static, nm_hist, miss_hist, nm[:TP], W, TP, late0, L, S, B_exp, chunks, lanes,
+        ids_static, nm_hist, miss_hist, nm[:TP], W, T, TP, late0, L, S, B_exp, chunks, lanes,
         peak, dev)
     verified["chain_rerun_state"] = None if chain is None else chain.pop("rerun_state_equal")
     stamps = None if args.no_chain else chain_stamps(
@@ -637,6 +640,16 @@ def main():
                                                    "prefetch"))
 
     traffic = _traffic()
+    if chain is not None:
+        achieved = chain["timed"]["gather_GBps"]
+        achieved_how = ("gathered bytes / what the gather launches add to the decode graph's "
+                        "time (HIP events on the launch stream around replays of the graph "
+                        "and of the same graph without its gathers, each from the same "
+                        "snapshot behind a stream hold; decode_chain.timed)")
+    else:
+        achieved = tw["achieved"]
+        achieved_how = ("gathered bytes / summed gather launch time, HIP events around each "
+                        "launch (achieved_events)")
 
     def rounded(v, n=3):
         return None if v is None else round(v, n)
@@ -689,9 +702,11 @@ def main():
         "gather_us_launch_without_miss": rounded(tw["zero_us"]),
         "link_peak": peak_detail,
         "roofline": {"bound": "host-link", "kernel": "gather_k",
-                     "achieved": round(tw["achieved"], 3),
+                     "achieved": round(achieved, 3),
                      "peak": round(peak, 3), "unit": "GB/s",
-                     "frac": round(tw["achieved"] / peak, 4),
+                     "frac": round(achieved / peak, 4),
+                     "achieved_events": round(tw["achieved"], 3),
+                     "frac_events": round(tw["achieved"] / peak, 4),
                      "frac_trace_pass": None if chain is None
                      else chain["trace_pass"]["gather_frac"],
                      "frac_steady_state": None if chain is None
@@ -708,16 +723,18 @@ def main():
                      else round(tw["with_miss"] / peak, 4),
                      "traffic": None if traffic is None else traffic["bytes_per_launch"],
                      "traffic_detail": traffic,
-                     "achieved_def": f"gathered bytes / summed gather kernel time over all "
-                                     f"launches, launches without a miss included, in the "
-                                     f"timed window (trace steps {W}..{T}"
-                                     f"{', a cold start' if W < 64 else ''}): {nseg} segments "
-                                     f"x {seg_len} steps x {L} layers re-run from snapshots, "
-                                     f"HIP events around each launch; "
-                                     f"achieved_launches_with_miss counts only launches that "
-                                     f"copy, gather_us_launch_without_miss is the rest's cost; "
-                                     f"steady_state is the same over the second half of the "
-                                     f"trace pass. frac_trace_pass and frac_steady_state: "
+                     "achieved_def": f"{achieved_how} in the timed window (trace steps "
+                                     f"{W}..{T}{', a cold start' if W < 64 else ''}). "
+                                     f"achieved_events: gathered bytes / summed gather "
+                                     f"launch time over all launches of the same window, "
+                                     f"launches without a miss included: {nseg} segments x "
+                                     f"{seg_len} steps x {L} layers re-run from snapshots, "
+                                     f"HIP events around each launch (which add the launch's "
+                                     f"dispatch); achieved_launches_with_miss counts only "
+                                     f"launches that copy, gather_us_launch_without_miss is "
+                                     f"the rest's cost; steady_state is the same over the "
+                                     f"second half of the trace pass. frac_trace_pass and "
+                                     f"frac_steady_state: "
                                      f"gathered bytes / what the gather nodes add to the "
                                      f"decode graph (its time minus the time of the same "
                                      f"graph without them) over trace steps {W}..{TP} and "
@@ -803,8 +820,8 @@ class Hold:
 
 
 def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, ids_dev,
-                ids_static, nm_hist, miss_hist, nm, W, TP, late0, L, S, B_exp, chunks, lanes,
-                peak, dev):
+                ids_static, nm_hist, miss_hist, nm, W, T, TP, late0, L, S, B_exp, chunks,
+                lanes, peak, dev):
     """What each node of the decode graph costs inside the chain, measured by substitution:
     the graph's step time against the same step with some of its nodes taken out or
     replaced, each replayed over the same trace steps behind stream holds. No events sit
@@ -825,8 +842,9 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
       empty node per layer   = (empty+gather - gathers) / (steps x L)
       gather per launch      = (full - policy) / (steps x L), and the gather's in-chain rate
                                is the gathered bytes over (full - policy).
-    The policy and full variants restart from the snapshot at step W; the full variant's
-    final state must equal the trace pass's (rerun_state_equal)."""
+    Each variant is timed per window: the timed steps W..T, the trace pass W..TP and its
+    second half late0..TP. The policy and full variants restart from the snapshot at step
+    W; the full variant's final state must equal the trace pass's (rerun_state_equal)."""
     i32 = torch.int32
     # recorded miss lists as gather inputs: row l = [n_miss, e0, s0, e1, s1, ...]
     rec_dev = torch.cat([nm_hist[:TP, :, None], miss_hist[:TP]], dim=2).contiguous()
@@ -870,7 +888,7 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
 
         if name in ("policy", "full"):
             st.restore(snap)
-        times[name] = hold.time(W, TP, enqueue, cuts=(late0,))
+        times[name] = hold.time(W, TP, enqueue, cuts=(late0, T))
         log(f"decode chain, {name}: {sum(x[2] for x in times[name]):.4f} s over steps "
             f"{W}..{TP}")
     rerun_equal = all(torch.equal(getattr(st, f), final[f]) for f in st.fields)
@@ -878,13 +896,13 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
     for name in ("gathers", "empty+gather", "policy", "gathers_again"):
         del variants[name]
 
-    def window(lo):
-        n = TP - lo
-        t = {k: sum(s for c0, _, s in v if c0 >= lo) for k, v in times.items()}
+    def window(lo, hi=TP):
+        n = hi - lo
+        t = {k: sum(s for c0, c1, s in v if c0 >= lo and c1 <= hi) for k, v in times.items()}
         per = 1e6 / (n * L)
-        moved = float(nm[lo:TP].sum()) * B_exp
+        moved = float(nm[lo:hi].sum()) * B_exp
         gather_s = t["full"] - t["policy"]
-        return {"trace_steps": [lo, TP],
+        return {"trace_steps": [lo, hi],
                 "ms_per_step": round(1e3 * t["full"] / n, 4),
                 "manage_remap_us_per_layer": round((t["full"] - t["gathers"]) * per, 3),
                 "noise_us_per_layer": round(abs(t["gathers_again"] - t["gathers"]) * per, 3),
@@ -895,10 +913,10 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
                 "gather_us_per_launch": round(gather_s * per, 3),
                 "gather_GBps": round(moved / gather_s / 1e9, 3),
                 "gather_frac": round(moved / gather_s / 1e9 / peak, 4),
-                "inserts": int(nm[lo:TP].sum()),
+                "inserts": int(nm[lo:hi].sum()),
                 "seconds": {k: round(v, 5) for k, v in t.items()}}
 
-    out = {"trace_pass": window(W), "steady_state": window(late0),
+    out = {"timed": window(W, T), "trace_pass": window(W), "steady_state": window(late0),
            "hold": hold.record(), "rerun_state_equal": rerun_equal,
            "manage_remap_def": f"what the policy+remap launch adds to the decode graph per "
                                f"layer, over trace steps {W}..{TP}: the graph's time minus "
@@ -906,7 +924,10 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
                                f"recorded miss lists), per layer-step; no events or "
                                f"profiler in the chain (decode_chain)",
            "def": chain_costs.__doc__.split("\n\n")[1].strip()}
-    tp, ss = out["trace_pass"], out["steady_state"]
+    tp, ss, tm = out["trace_pass"], out["steady_state"], out["timed"]
+    log(f"decode chain over the timed steps {W}..{T}: gather {tm['gather_GBps']} GB/s "
+        f"({tm['gather_frac']}), {tm['gather_us_per_launch']} us per launch, policy+remap "
+        f"{tm['manage_remap_us_per_layer']} us/layer")
     log(f"decode chain over steps {W}..{TP}: policy+remap {tp['manage_remap_us_per_layer']} "
         f"us/layer (noise {tp['noise_us_per_layer']}, empty node {tp['empty_node_us']}, "
         f"policy-only graph "
