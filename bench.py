@@ -707,6 +707,20 @@ def main():
                      "frac": round(achieved / peak, 4),
                      "achieved_events": round(tw["achieved"], 3),
                      "frac_events": round(tw["achieved"] / peak, 4),
+                     # the metric's other two parts, as scalars beside the gather's
+                     "policy_kernel": "manage_k (policy step + fused remap, one wavefront)",
+                     "policy_bound": "latency",
+                     "policy_us_per_layer": manage_us,
+                     "policy_kernel_us_in_chain":
+                         None if stamps is None
+                         else stamps["chain"]["trace_pass"]["policy_us"]["mean"],
+                     "policy_empty_node_us":
+                         None if chain is None else chain["trace_pass"]["empty_node_us"],
+                     "policy_target_us": 10.0,
+                     "policy_def": "us/layer the launch adds to the decode graph (node "
+                                   "substitution); kernel: clock stamps; empty node: same "
+                                   "place",
+                     "hit_rate_trace_pass": trace_pass["hit_rate"],
                      "frac_trace_pass": None if chain is None
                      else chain["trace_pass"]["gather_frac"],
                      "frac_steady_state": None if chain is None
