@@ -784,6 +784,13 @@ def main():
         sys.exit(1)
 
 
+def chunk_points(lo, hi, chunk, cuts=()):
+    """Boundaries of the timed chunks of steps [lo, hi): every multiple of `chunk` inside,
+    each cut inside, and both ends; sorted."""
+    return sorted({lo, hi} | {c for c in cuts if lo < c < hi} |
+                  set(range((lo // chunk + 1) * chunk, hi, chunk)))
+
+
 class Hold:
     """Times short GPU work with stream holds: each chunk of steps is queued behind a spin
     kernel on the current stream, so the GPU runs the chunk back to back instead of at the
@@ -807,8 +814,7 @@ class Hold:
         """Runs enqueue(t) for t in [lo, hi) in chunks that end at multiples of `chunk` and
         at each of `cuts`; returns [(c0, c1, GPU seconds of chunk [c0, c1))]."""
         torch = self.torch
-        pts = sorted({lo, hi} | {c for c in cuts if lo < c < hi} |
-                     set(range((lo // chunk + 1) * chunk, hi, chunk)))
+        pts = chunk_points(lo, hi, chunk, cuts)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         out = []
         self.hold_us = self.first_us
@@ -831,6 +837,30 @@ class Hold:
     def record(self):
         return {"chunks": self.chunks, "late_chunks": self.late,
                 "spin_cycles_per_us": round(self.cyc_per_us, 1)}
+
+
+def substitution_window(times, lo, hi, nm, L, B_exp, peak):
+    """The decode chain's per-node costs over trace steps [lo, hi) from the substitution
+    variants' timed chunks: times[variant] = [(c0, c1, GPU seconds of chunk [c0, c1))], with
+    variants full, gathers, gathers_again, empty+gather and policy (chain_costs); only the
+    chunks that lie inside the window count. nm[t, l] is the inserts of step t, layer l."""
+    n = hi - lo
+    t = {k: sum(s for c0, c1, s in v if c0 >= lo and c1 <= hi) for k, v in times.items()}
+    per = 1e6 / (n * L)
+    moved = float(nm[lo:hi].sum()) * B_exp
+    gather_s = t["full"] - t["policy"]
+    return {"trace_steps": [lo, hi],
+            "ms_per_step": round(1e3 * t["full"] / n, 4),
+            "manage_remap_us_per_layer": round((t["full"] - t["gathers"]) * per, 3),
+            "noise_us_per_layer": round(abs(t["gathers_again"] - t["gathers"]) * per, 3),
+            "empty_node_us": round((t["empty+gather"] - t["gathers"]) * per, 3),
+            "manage_remap_over_empty_node_us": round((t["full"] - t["empty+gather"]) * per, 3),
+            "policy_graph_us_per_layer": round(t["policy"] * per, 3),
+            "gather_us_per_launch": round(gather_s * per, 3),
+            "gather_GBps": round(moved / gather_s / 1e9, 3),
+            "gather_frac": round(moved / gather_s / 1e9 / peak, 4),
+            "inserts": int(nm[lo:hi].sum()),
+            "seconds": {k: round(v, 5) for k, v in t.items()}}
 
 
 def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, ids_dev,
@@ -911,24 +941,7 @@ def chain_costs(torch, lib, hold, graph, m_args, gather_args, st, snap, final, i
         del variants[name]
 
     def window(lo, hi=TP):
-        n = hi - lo
-        t = {k: sum(s for c0, c1, s in v if c0 >= lo and c1 <= hi) for k, v in times.items()}
-        per = 1e6 / (n * L)
-        moved = float(nm[lo:hi].sum()) * B_exp
-        gather_s = t["full"] - t["policy"]
-        return {"trace_steps": [lo, hi],
-                "ms_per_step": round(1e3 * t["full"] / n, 4),
-                "manage_remap_us_per_layer": round((t["full"] - t["gathers"]) * per, 3),
-                "noise_us_per_layer": round(abs(t["gathers_again"] - t["gathers"]) * per, 3),
-                "empty_node_us": round((t["empty+gather"] - t["gathers"]) * per, 3),
-                "manage_remap_over_empty_node_us":
-                    round((t["full"] - t["empty+gather"]) * per, 3),
-                "policy_graph_us_per_layer": round(t["policy"] * per, 3),
-                "gather_us_per_launch": round(gather_s * per, 3),
-                "gather_GBps": round(moved / gather_s / 1e9, 3),
-                "gather_frac": round(moved / gather_s / 1e9 / peak, 4),
-                "inserts": int(nm[lo:hi].sum()),
-                "seconds": {k: round(v, 5) for k, v in t.items()}}
+        return substitution_window(times, lo, hi, nm, L, B_exp, peak)
 
     out = {"timed": window(W, T), "trace_pass": window(W), "steady_state": window(late0),
            "hold": hold.record(), "rerun_state_equal": rerun_equal,

@@ -113,3 +113,40 @@ def test_stamps_library_exports():
     for name in ("stamped_manage_remap", "stamped_gather", "stamped_empty",
                  "stamped_clock_khz"):
         assert hasattr(h, name), name
+
+
+def test_substitution_windows_count_only_their_chunks():
+    """The decode chain's figures per window: chunks end at every cut, so the timed window
+    (steps 5..25 inside a pass 5..4096 timed in chunks of 16) sums exactly its own steps,
+    and the per-node costs come out of synthetic chunk times whose per-step costs are
+    known: a policy node adding 2.4 us, an empty node 1.5 us, the gathers moving each
+    step's inserts at a fixed rate plus 1.5 us per node."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    pts = bench.chunk_points(5, 4096, 16, cuts=(2048, 25))
+    assert pts[0] == 5 and pts[-1] == 4096 and 25 in pts and 2048 in pts
+    assert pts[:4] == [5, 16, 25, 32]
+    assert bench.chunk_points(5, 25, 16, cuts=(25, 4000)) == [5, 16, 25]
+
+    L, B, rate = 48, 4732928, 55e9
+    nm = np.zeros((4096, L), np.int64)
+    nm[5:25] = 2
+    nm[25:] = np.arange(4096 - 25)[:, None] % 2
+    g = nm.sum(1) * B / rate + L * 1.5e-6           # gathers-only graph, per step
+    per_step = {"gathers": g, "gathers_again": g, "empty+gather": g + L * 1.5e-6,
+                "full": g + L * 2.4e-6, "policy": np.full(4096, L * 2.5e-6)}
+    times = {k: [(c0, c1, float(v[c0:c1].sum())) for c0, c1 in zip(pts[:-1], pts[1:])]
+             for k, v in per_step.items()}
+    for lo, hi in ((5, 25), (5, 4096), (2048, 4096)):
+        w = bench.substitution_window(times, lo, hi, nm, L, B, 57.6)
+        assert w["trace_steps"] == [lo, hi]
+        assert w["inserts"] == int(nm[lo:hi].sum())
+        assert w["manage_remap_us_per_layer"] == 2.4
+        assert w["empty_node_us"] == 1.5
+        assert w["manage_remap_over_empty_node_us"] == 0.9
+        assert w["noise_us_per_layer"] == 0.0
+        assert w["policy_graph_us_per_layer"] == 2.5
+        gather_s = float((g[lo:hi] - L * 0.1e-6).sum())
+        assert w["gather_GBps"] == round(float(nm[lo:hi].sum()) * B / gather_s / 1e9, 3)
+        assert abs(w["gather_us_per_launch"] - gather_s * 1e6 / ((hi - lo) * L)) < 1e-3
