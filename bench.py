@@ -1476,10 +1476,12 @@ PREFETCH_RUNS = (
     {"accuracy": 0.8, "lookahead": 1},
     {"accuracy": 0.8, "lookahead": 1, "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2},
+    {"accuracy": 0.8, "lookahead": 3},
     {"accuracy": 0.8, "lookahead": 1, "budget": 1},
     {"accuracy": 0.8, "lookahead": 1, "errors": "routed"},
     {"accuracy": 0.8, "lookahead": 1, "errors": "routed", "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2, "errors": "routed"},
+    {"accuracy": 0.8, "lookahead": 3, "errors": "routed"},
 )
 
 
