@@ -55,7 +55,8 @@ Printed (one JSON line on stdout; the run exits 1 if any verification fails):
                routes elsewhere in the trace), one to four layers ahead, the prefetch step
                launched on its own (expert_cache_prefetch) or inside the policy launch
                (expert_cache_manage_remap_prefetch), the copy forked after the policy launch
-               or after the layer's gather, and an insert budget of one
+               or after the layer's gather, or two layers' copies forked together after
+               every second policy launch, and an insert budget of one
   fused        expert_cache_fused (the LRU step plus both moe_align_block_size outputs,
                block size 16) per layer-step in graph replay, 8 layers x 256 steps of three
                workloads from a cold start; cpu_baseline.fused_us_per_layer_step times the
@@ -1473,6 +1474,8 @@ PREFETCH_RUNS = (
     {"accuracy": 1.0, "lookahead": 2},
     {"accuracy": 1.0, "lookahead": 3},
     {"accuracy": 1.0, "lookahead": 4},
+    {"accuracy": 1.0, "lookahead": 3, "pair": True},
+    {"accuracy": 1.0, "lookahead": 4, "pair": True},
     {"accuracy": 0.8, "lookahead": 1},
     {"accuracy": 0.8, "lookahead": 1, "late_fork": True},
     {"accuracy": 0.8, "lookahead": 2},
@@ -1518,7 +1521,10 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
               compute(l). The copy of layer l+d's prefetched experts
               (expert_cache_gather_live, on a side stream) forks right after the policy
               launch (the default, as ExpertSlotCache does) or, with "late_fork", after
-              gather(l), so that it does not share the host link with gather(l).
+              gather(l), so that it does not share the host link with gather(l); with
+              "pair", after every second policy launch, carrying the copies of the two
+              layers prefetched since (half the cross-stream edges; half the copies start
+              a layer later).
     The real step of a layer settles its pending prefetch installs: routed ones stay, the
     others are dropped, and their live copy stops.
 
@@ -1526,8 +1532,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     CU (C = 0: no compute, so prefetch has nothing to hide behind). Predictions come from
     _predictions; accuracy 1.0 is an upper bound no real predictor reaches. Each run is a
     dict of accuracy (absent: no prefetch), lookahead, one_launch (default True), late_fork
-    (default False), budget (inserts per prefetch step, default S) and errors ("uniform",
-    the default, or "routed").
+    (default False), pair (default False), budget (inserts per prefetch step, default S) and
+    errors ("uniform", the default, or "routed").
 
     Checked: every run's per-step n_miss and miss list of each layer's real step and of its
     prefetch step, and the final state, against the oracle's prefetch and policy steps
@@ -1600,15 +1606,23 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
     gr_args = [tuple(g_args[l][:18]) + (st.row("miss", l), _row(nm_static, l), chunks, lanes)
                for l in range(L)]
 
-    def launch(cur, la, one, late, budget, spin):
+    def launch(cur, la, one, late, budget, spin, pair=False):
         c = ctypes.c_void_p(cur.cuda_stream)
         sd = ctypes.c_void_p(side.cuda_stream)
         pa = [a[:4] + (budget,) + a[5:] for a in p_args]
+        held = []  # with pair: prefetched layers whose copy waits for the next fork
 
         def copy(l):
+            if pair and l >= la:
+                held.append(l)
+                if len(held) < 2 and l < L - 1:
+                    return 0
             side.wait_stream(cur)
-            rc = lib.expert_cache_gather_live(*gp_args[l], sd)
-            done[l].record(side)
+            rc = 0
+            for m in (held if pair and l >= la else [l]):
+                rc |= lib.expert_cache_gather_live(*gp_args[m], sd)
+                done[m].record(side)
+            held.clear()
             return rc
 
         rc = 0
@@ -1650,6 +1664,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             q = run.get("accuracy")
             la = run.get("lookahead", 0) if q is not None else 0
             one, late = run.get("one_launch", True), run.get("late_fork", False)
+            pair = run.get("pair", False)
             budget = run.get("budget") or S
             errors = run.get("errors", "uniform")
             pred = None if q is None else (ids_np[W:W + K].copy() if q >= 1.0 else
@@ -1668,7 +1683,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                launch(torch.cuda.current_stream(), la, one, late, budget, int(C * cyc_per_us))
+                launch(torch.cuda.current_stream(), la, one, late, budget, int(C * cyc_per_us),
+                       pair)
             torch.cuda.synchronize()
             wall0 = time.perf_counter()
             a.record()
@@ -1717,7 +1733,8 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                         "lookahead_layers": la, "one_launch": one if la else None,
                         "copy_fork": (None if not la else
                                       "after the layer's gather" if late else
-                                      "after the policy launch"),
+                                      "after every second policy launch, two layers' "
+                                      "copies" if pair else "after the policy launch"),
                         "insert_budget": budget if q is not None else None,
                         "ms_per_step": round(ms, 4),
                         "speedup_vs_no_prefetch": round(base_ms[C] / ms, 4),
@@ -1730,6 +1747,7 @@ def prefetch_leg(torch, np, lib, ids_np, ids_dev, g_args, snap, L, E, S, mk, pol
                 f"{q} ({errors} errors), lookahead {la}"
                 f"{', one launch' if one else ', two launches'}"
                 f"{', copy forked after the gather' if late else ''}"
+                f"{', copies forked two layers at a time' if pair else ''}"
                 f"{f', budget {budget}' if budget < S else ''}")
             log(f"prefetch leg, compute {C} us/layer, predictor {desc}: {ms:.3f} ms/step "
                 f"({base_ms[C] / ms:.3f}x), {int(pn.sum())} prefetched ({used} used), "
